@@ -1,0 +1,215 @@
+"""Benchmark of the verify round's dominant kernel on one MI355X.
+
+One step = the verify-attention work of one verification round of
+Qwen3-0.6B: 28 layers, each a paged verify-attention
+call over that layer's own KV cache (B=8, 16Q/8KV heads, d=128, bf16,
+256-token pages, contexts uniform in [1200, 1300], K=8 drafts so 9 query
+rows per sequence).  The 28 distinct caches (~1.9 GB) rotate the working set
+far past the 256 MB Infinity Cache, so the bandwidth is HBM bandwidth.
+
+Prints one JSON line (rank 0).  ``value`` = algorithmic bytes per
+verify-attention call / average call duration, the duration from HIP
+events on the stream the kernels run on, over the timed steps.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+from naivllm_amd.layers.attention import paged_attention_verify  # noqa: E402
+from naivllm_amd.utils import synth  # noqa: E402
+
+METRIC = "verify-attn HBM GB/s (% of peak) + accepted tok/s, Qwen3-0.6B K=8 b1/b8"
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def algorithmic_bytes(ctx_lens, T, H, Hkv, D, elt, max_blocks) -> int:
+    """KV read once + Q read + O written + metadata (block table, context
+    lengths, cu_seqlens, positions)."""
+    B = len(ctx_lens)
+    kv = sum(ctx_lens) * Hkv * D * 2 * elt
+    return kv + 2 * T * H * D * elt + 4 * B * max_blocks + 8 * B + 4 * (B + 1) + 8 * T
+
+
+def algorithmic_flops(ctx_lens, q_rows_per_seq, H, D) -> int:
+    return 4 * q_rows_per_seq * D * H * sum(ctx_lens)
+
+
+class Workload:
+    def __init__(self, config: int, layers: int, seed: int, device):
+        self.config = config
+        if config == 2:
+            self.B, self.H, self.Hkv, self.D, self.bs, self.K = 8, 16, 8, 128, 256, 8
+            self.ctx = synth.config2_ctx_lens(seed, self.B)
+            self.layers = layers
+            pool_pages = 64
+            name = "verify-attention, Qwen3-0.6B layer shape, b8 bf16, L~U[1200,1300], K=8, 28 layers"
+        elif config == 4:
+            self.B, self.H, self.Hkv, self.D, self.bs, self.K = 16, 32, 8, 128, 256, 8
+            self.ctx = [int(x) for x in synth.randint(seed, 7, 16, 16384, 32769)]
+            self.layers = max(2, min(layers, 2))
+            pool_pages = 1700
+            name = "verify-attention, Qwen3-8B layer shape, b16 bf16, L~U[16k,32k], K=8, 2 rotating pools"
+        else:
+            raise SystemExit(f"config {config} is not a bench workload (2 or 4)")
+        self.name = name
+        self.rows = self.K + 1
+        self.T = self.B * self.rows
+        pages = [(c + self.bs - 1) // self.bs for c in self.ctx]
+        self.max_blocks = max(pages)
+        perm = synth.randperm(seed, 1, pool_pages)
+        bt = np.full((self.B, self.max_blocks), -1, dtype=np.int32)
+        off = 0
+        for b in range(self.B):
+            bt[b, :pages[b]] = perm[off:off + pages[b]]
+            off += pages[b]
+        g = torch.Generator(device=device)
+        g.manual_seed(seed)
+        shape = (pool_pages, self.bs, self.Hkv, self.D)
+        self.k_caches = [torch.randn(shape, generator=g, device=device, dtype=torch.bfloat16) for _ in range(self.layers)]
+        self.v_caches = [torch.randn(shape, generator=g, device=device, dtype=torch.bfloat16) for _ in range(self.layers)]
+        self.q = torch.randn(self.T, self.H, self.D, generator=g, device=device, dtype=torch.bfloat16)
+        self.out = torch.empty_like(self.q)
+        self.block_tables = torch.from_numpy(bt).to(device)
+        self.context_lens = torch.tensor(self.ctx, dtype=torch.int64, device=device)
+        self.cu = torch.arange(0, self.T + 1, self.rows, dtype=torch.int32, device=device)
+        pos = np.concatenate([np.arange(c - self.rows, c) for c in self.ctx])
+        self.positions = torch.from_numpy(pos).to(device)
+        self.scale = 1.0 / np.sqrt(self.D)
+        self.bytes = algorithmic_bytes(self.ctx, self.T, self.H, self.Hkv, self.D, 2, self.max_blocks)
+        self.flops = algorithmic_flops(self.ctx, self.rows, self.H, self.D)
+
+    def call(self, layer: int, split: int):
+        paged_attention_verify(self.q, self.k_caches[layer], self.v_caches[layer], self.block_tables,
+                               self.context_lens, self.cu, self.positions, self.scale, self.H, self.Hkv, self.D,
+                               self.bs, 16, max_q_len=self.rows, kv_split_tokens=split, out=self.out)
+
+    def step(self, split: int):
+        for layer in range(self.layers):
+            self.call(layer, split)
+
+
+def cpu_baseline(seconds: float) -> dict:
+    """The torch-on-CPU restatement of the same verify-attention call
+    (config 2 shape, one layer), timed on this host's cores."""
+    from oracle import torch_cpu
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    vb_ctx = synth.config2_ctx_lens(2, 8)
+    B, H, Hkv, D, bs, rows = 8, 16, 8, 128, 256, 9
+    pages = [(c + bs - 1) // bs for c in vb_ctx]
+    g = torch.Generator().manual_seed(2)
+    nb = sum(pages) + 4
+    kc = torch.randn(nb, bs, Hkv, D, generator=g).to(torch.bfloat16)
+    vc = torch.randn(nb, bs, Hkv, D, generator=g).to(torch.bfloat16)
+    q = torch.randn(B * rows, H, D, generator=g).to(torch.bfloat16)
+    bt = torch.full((B, max(pages)), -1, dtype=torch.int32)
+    off = 0
+    for b in range(B):
+        bt[b, :pages[b]] = torch.arange(off, off + pages[b], dtype=torch.int32)
+        off += pages[b]
+    ctx = torch.tensor(vb_ctx)
+    cu = torch.arange(0, B * rows + 1, rows, dtype=torch.int32)
+    pos = torch.cat([torch.arange(c - rows, c) for c in vb_ctx])
+    args = (q, kc, vc, bt, ctx, cu, pos, 1 / np.sqrt(D), H, Hkv)
+    torch_cpu.paged_verify_attention(*args)  # warm
+    n, t0 = 0, time.perf_counter()
+    while True:
+        torch_cpu.paged_verify_attention(*args)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    nbytes = algorithmic_bytes(vb_ctx, B * rows, H, Hkv, D, 2, max(pages))
+    return {"value": round(nbytes * n / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{n} calls of the config-2 verify-attention (b8 bf16, one layer) in {el:.1f} s, "
+                      f"torch CPU restatement of layers/attention.py:328-363 on {platform.processor() or 'host'} "
+                      f"with {threads} threads"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=2)
+    ap.add_argument("--layers", type=int, default=28)
+    ap.add_argument("--split", type=int, default=0, help="keys per workgroup split (0 = automatic)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--seed", type=int, default=2)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus})",
+              file=sys.stderr)
+        raise SystemExit(2)
+    if not torch.cuda.is_available():
+        raise SystemExit("bench.py needs a GPU")
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    wl = Workload(args.config, args.layers, args.seed, dev)
+    print(f"[bench] workload: {wl.name}; ctx={wl.ctx}", file=sys.stderr, flush=True)
+    for _ in range(args.warmup):
+        wl.step(args.split)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        wl.step(args.split)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms_total = e0.elapsed_time(e1)
+    ms_per_step = ms_total / args.steps
+    calls = args.steps * wl.layers
+    us_per_call = ms_total * 1e3 / calls
+    gbs = wl.bytes / (us_per_call * 1e-6) / 1e9
+    tflops = wl.flops / (us_per_call * 1e-6) / 1e12
+    print(f"[bench] {calls} calls, {us_per_call:.2f} us/call, {gbs:.1f} GB/s, {tflops:.1f} TFLOP/s",
+          file=sys.stderr, flush=True)
+
+    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+    line = {
+        "metric": METRIC,
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) Q/K/V, seeded page permutation)",
+        "config": {"workload": wl.name, "batch": wl.B, "num_heads": wl.H, "num_kv_heads": wl.Hkv,
+                   "head_dim": wl.D, "block_size": wl.bs, "K": wl.K, "context_lens": wl.ctx,
+                   "layers_per_step": wl.layers, "kv_split_tokens": args.split},
+        "pct_of_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+        "us_per_call": round(us_per_call, 3),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_call": wl.bytes, "mfma_tflops": round(tflops, 2),
+                     "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 5)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

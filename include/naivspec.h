@@ -1,0 +1,91 @@
+/*
+ * naivspec.h — C ABI of libnaivspec.so, the MI355X (gfx950) kernels of the
+ * speculative-decoding verification round.
+ *
+ * Conventions shared by every entry point:
+ *   - All tensor arguments are caller-owned device pointers, row-major and
+ *     contiguous unless a stride argument says otherwise.
+ *   - `stream` is a hipStream_t passed as void* (torch's
+ *     torch.cuda.current_stream().cuda_stream); work is enqueued there and
+ *     never synchronised, so every call can be captured into a hipGraph.
+ *   - No entry point allocates device memory.  Scratch comes in through an
+ *     explicit `workspace` pointer sized by the matching *_workspace_size().
+ *   - Return value: 0 on success, a negative NSV_ERR_* code for a rejected
+ *     argument (nothing was launched), or a positive hipError_t when the
+ *     launch itself failed.
+ *   - dtype codes: NSV_F32 = 0, NSV_BF16 = 1.
+ *
+ * Each declaration cites the reference interface (Hongli-xd/Naivllm,
+ * src/myvllm/...) whose behaviour it reproduces.
+ */
+#ifndef NAIVSPEC_H
+#define NAIVSPEC_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NSV_F32 0
+#define NSV_BF16 1
+
+#define NSV_OK 0
+#define NSV_ERR_ARG (-1)         /* null pointer, negative size, bad dtype  */
+#define NSV_ERR_UNSUPPORTED (-2) /* shape outside what the kernels handle   */
+#define NSV_ERR_WORKSPACE (-3)   /* workspace pointer null or too small     */
+
+/* Library version (major*10000 + minor*100 + patch). */
+int nsv_version(void);
+
+/* Human-readable text for a return code of any nsv_* function. */
+const char* nsv_error_string(int code);
+
+/*
+ * Paged multi-token verify attention.
+ * Replaces layers/attention.py:615-668 (paged_attention_verify) and its
+ * Triton kernel :522-612.  For query row r of sequence b (rows
+ * cu_seqlens_q[b] .. cu_seqlens_q[b+1]-1) and head h:
+ *     out[r,h,:] = softmax_j(scale * q[r,h,:] . k_j) V_j
+ * over keys j <= positions[r], j < context_lens[b], whose page
+ * block_tables[b, j / block_size] is >= 0; kv head = h / (H / Hkv).
+ * Rows with positions[r] < 0 (inert padding) are written as zeros.
+ *   q, out        [T, H, D]              dtype
+ *   k_cache/v_cache  [num_blocks, block_size, Hkv, D] (one layer), dtype
+ *   block_tables  [B, max_blocks] int32, -1 padded
+ *   context_lens  [B] int64; cu_seqlens_q [B+1] int32; positions [T] int64
+ *   max_q_len     >= every cu_seqlens_q[b+1]-cu_seqlens_q[b] (host-known,
+ *                 as the reference computes block_m from seqlens_q)
+ *   kv_split_tokens  keys per workgroup split (multiple of 128); 0 = auto
+ * Supported: D in {64, 128}; H % Hkv == 0; (H/Hkv)*max_q_len <= 64.
+ */
+size_t nsv_verify_attention_workspace_size(int B, int H, int Hkv, int D,
+                                           int block_size, int max_blocks,
+                                           int max_q_len, int dtype,
+                                           int kv_split_tokens);
+int nsv_verify_attention(void* out, const void* q, const void* k_cache,
+                         const void* v_cache, const int32_t* block_tables,
+                         const int64_t* context_lens,
+                         const int32_t* cu_seqlens_q, const int64_t* positions,
+                         float scale, int B, int T, int H, int Hkv, int D,
+                         int block_size, int max_blocks, int max_q_len,
+                         int dtype, int kv_split_tokens, void* workspace,
+                         size_t workspace_bytes, void* stream);
+
+/*
+ * Paged KV scatter.
+ * Replaces layers/attention.py:71-112 (store_kvcache) and its kernel :9-68:
+ *   k_cache[s / bs, s % bs, :, :] = key[t];  v_cache[...] = value[t]
+ * for s = slot_mapping[t] >= 0; rows with slot -1 are skipped.
+ *   key/value [T, Hkv, D]; caches [num_blocks, block_size, Hkv, D]
+ */
+int nsv_store_kv(const void* key, const void* value, void* k_cache,
+                 void* v_cache, const int64_t* slot_mapping, int T, int Hkv,
+                 int D, int block_size, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NAIVSPEC_H */

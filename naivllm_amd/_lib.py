@@ -1,0 +1,86 @@
+"""ctypes binding of libnaivspec.so (declarations in include/naivspec.h).
+
+The library is loaded after ``import torch`` so that its HIP runtime
+dependency (libamdhip64.so.7) resolves to the copy torch already loaded:
+one runtime per process, so torch's streams and device pointers are valid
+inside the library.  There is no fallback: if the library is missing every
+operator raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (must be imported before the library is loaded)
+
+LIB_NAME = "libnaivspec.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+NSV_F32 = 0
+NSV_BF16 = 1
+
+_c_int, _c_f32, _c_vp, _c_size = ctypes.c_int, ctypes.c_float, ctypes.c_void_p, ctypes.c_size_t
+_c_i64 = ctypes.c_int64
+
+# name -> (restype, argtypes); every symbol the header declares.
+SIGNATURES: dict[str, tuple] = {
+    "nsv_version": (_c_int, []),
+    "nsv_error_string": (ctypes.c_char_p, [_c_int]),
+    "nsv_verify_attention_workspace_size": (
+        _c_size, [_c_int] * 9),
+    "nsv_verify_attention": (
+        _c_int,
+        [_c_vp] * 8 + [_c_f32] + [_c_int] * 10 + [_c_vp, _c_size, _c_vp]),
+    "nsv_store_kv": (_c_int, [_c_vp] * 5 + [_c_int] * 5 + [_c_vp]),
+}
+
+_lib = None
+
+
+class NaivspecError(RuntimeError):
+    """A kernel launch failed inside libnaivspec.so."""
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with naivllm_amd.build.build_library() "
+                "(or __graft_entry__.build()); there is no non-HIP fallback")
+        handle = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    """Map a library return code onto the reference's error behaviour:
+    rejected arguments raise ValueError (the reference asserts / raises
+    ValueError on bad inputs), launch failures raise NaivspecError."""
+    if rc == 0:
+        return
+    msg = lib().nsv_error_string(rc).decode()
+    if rc < 0:
+        raise ValueError(f"{what}: {msg} (code {rc})")
+    raise NaivspecError(f"{what}: HIP error {rc}: {msg}")
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.float32:
+        return NSV_F32
+    if dtype == torch.bfloat16:
+        return NSV_BF16
+    raise ValueError(f"unsupported dtype {dtype}; libnaivspec handles float32 and bfloat16")
+
+
+def stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()

@@ -1,0 +1,183 @@
+"""Verify-attention and KV-store operators with the reference's signatures.
+
+Drop-in for ``paged_attention_verify`` and ``store_kvcache`` of
+src/myvllm/layers/attention.py (:615-668 and :71-112) and for the verify
+branch of ``Attention.forward`` (:689-731).  Both operators launch the
+gfx950 kernels of libnaivspec.so on torch's current stream; there is no
+PyTorch fallback.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from naivllm_amd import _lib
+from naivllm_amd.utils.context import get_context
+
+_INDEX_DTYPES = {
+    "block_tables": torch.int32,
+    "context_lens": torch.int64,
+    "cu_seqlens_q": torch.int32,
+    "positions": torch.int64,
+    "slot_mapping": torch.int64,
+}
+
+
+def _as(t: torch.Tensor, name: str) -> torch.Tensor:
+    want = _INDEX_DTYPES[name]
+    if t.dtype != want:
+        t = t.to(want)
+    return t if t.is_contiguous() else t.contiguous()
+
+
+def _check_cache(cache: torch.Tensor, name: str) -> tuple[int, int, int, int]:
+    if cache.dim() != 4:
+        raise ValueError(f"{name} must be (num_blocks, block_size, num_kv_heads, head_dim), got {tuple(cache.shape)}")
+    if not cache.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return tuple(cache.shape)
+
+
+def verify_attention_workspace_bytes(batch_size: int, num_heads: int, num_kv_heads: int, head_dim: int,
+                                     block_size: int, max_num_blocks: int, max_q_len: int,
+                                     dtype: torch.dtype, kv_split_tokens: int = 0) -> int:
+    return int(_lib.lib().nsv_verify_attention_workspace_size(
+        batch_size, num_heads, num_kv_heads, head_dim, block_size, max_num_blocks, max_q_len,
+        _lib.dtype_code(dtype), kv_split_tokens))
+
+
+def paged_attention_verify(
+    query: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    block_tables: torch.Tensor,
+    context_lens: torch.Tensor,
+    cu_seqlens_q: torch.Tensor,
+    positions: torch.Tensor,
+    scale: float,
+    num_heads: int,
+    num_kv_heads: int,
+    head_dim: int,
+    block_size: int,
+    block_m: int,
+    *,
+    max_q_len: int | None = None,
+    kv_split_tokens: int = 0,
+    out: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Verify a chunk of drafted tokens against the paged KV cache.
+
+    Same arguments and result as the reference (layers/attention.py:615-668):
+      query (T, H, D); k_cache/v_cache (num_blocks, block_size, Hkv, D);
+      block_tables (B, max_num_blocks), -1 padded; context_lens (B,);
+      cu_seqlens_q (B+1,); positions (T,), -1 marks an inert pad row;
+      block_m >= every per-sequence query length.
+    Returns (T, H, D) in query's dtype.  Keyword-only extras: ``max_q_len``
+    (a tighter bound than block_m: fewer padded MFMA rows and partials),
+    ``kv_split_tokens`` (keys per workgroup split, 0 = automatic) and ``out``
+    (a preallocated result).  Rows at position -1 come back as zeros (the
+    reference leaves them meaningless; nothing reads them).
+    """
+    if query.dim() != 3 or query.shape[1] != num_heads or query.shape[2] != head_dim:
+        raise ValueError(f"query must be (T, {num_heads}, {head_dim}), got {tuple(query.shape)}")
+    nb, bs, hkv, d = _check_cache(k_cache, "k_cache")
+    if tuple(v_cache.shape) != (nb, bs, hkv, d) or not v_cache.is_contiguous():
+        raise ValueError("k_cache and v_cache must have the same contiguous shape")
+    if bs != block_size or hkv != num_kv_heads or d != head_dim:
+        raise ValueError("cache shape disagrees with block_size / num_kv_heads / head_dim")
+    if query.dtype != k_cache.dtype or v_cache.dtype != k_cache.dtype:
+        raise ValueError("query and caches must share one dtype")
+    if not query.is_cuda:
+        raise ValueError("paged_attention_verify runs on the GPU; query is on the CPU")
+    query = query.contiguous()
+    block_tables = _as(block_tables, "block_tables")
+    context_lens = _as(context_lens, "context_lens")
+    cu_seqlens_q = _as(cu_seqlens_q, "cu_seqlens_q")
+    positions = _as(positions, "positions")
+    batch_size, max_num_blocks = block_tables.shape
+    qlen_bound = int(max_q_len if max_q_len is not None else block_m)
+    code = _lib.dtype_code(query.dtype)
+    if out is None:
+        out = torch.empty_like(query)
+    h = _lib.lib()
+    ws_bytes = int(h.nsv_verify_attention_workspace_size(
+        batch_size, num_heads, num_kv_heads, head_dim, block_size, max_num_blocks, qlen_bound, code,
+        kv_split_tokens))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=query.device) if ws_bytes else None
+    rc = h.nsv_verify_attention(
+        out.data_ptr(), query.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+        block_tables.data_ptr(), context_lens.data_ptr(), cu_seqlens_q.data_ptr(), positions.data_ptr(),
+        float(scale), batch_size, query.shape[0], num_heads, num_kv_heads, head_dim, block_size,
+        max_num_blocks, qlen_bound, code, kv_split_tokens,
+        _lib.ptr(ws), ws_bytes, _lib.stream_ptr(query.device))
+    _lib.check(rc, "paged_attention_verify")
+    return out
+
+
+def store_kvcache(
+    key: torch.Tensor,
+    value: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    slot_mapping: torch.Tensor,
+    block_size: int,
+) -> None:
+    """Scatter (T, Hkv, D) key/value rows into the paged caches at
+    ``slot_mapping`` (slot -1 = skip), as layers/attention.py:71-112."""
+    num_tokens, num_kv_heads, head_dim = key.shape
+    key = key.contiguous()
+    value = value.contiguous()
+    if k_cache.shape != v_cache.shape:
+        raise ValueError("K and V cache shapes must match")
+    if slot_mapping.numel() != num_tokens:
+        raise ValueError("Slot mapping size must match number of tokens")
+    nb, bs, hkv, d = _check_cache(k_cache, "k_cache")
+    if not v_cache.is_contiguous():
+        raise ValueError("v_cache must be contiguous")
+    if (bs, hkv, d) != (block_size, num_kv_heads, head_dim):
+        raise ValueError("cache shape disagrees with key shape / block_size")
+    if key.dtype != k_cache.dtype or value.dtype != v_cache.dtype:
+        raise ValueError("key/value and caches must share one dtype")
+    slot_mapping = _as(slot_mapping, "slot_mapping")
+    rc = _lib.lib().nsv_store_kv(
+        key.data_ptr(), value.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), slot_mapping.data_ptr(),
+        num_tokens, num_kv_heads, head_dim, block_size, _lib.dtype_code(key.dtype),
+        _lib.stream_ptr(key.device))
+    _lib.check(rc, "store_kvcache")
+
+
+class Attention(nn.Module):
+    """Verify-mode attention layer (layers/attention.py:674-731): writes this
+    step's K/V into the paged cache, then runs verify attention for the rows
+    described by the global Context.  Only the verify / decode (q_len 1)
+    modes of the round are served here."""
+
+    def __init__(self, num_heads: int, head_dim: int, scale: float = 1.0, num_kv_heads: int | None = None,
+                 block_size: int = 16):
+        super().__init__()
+        self.num_heads = num_heads
+        self.head_dim = head_dim
+        self.scale = scale
+        self.num_kv_heads = num_kv_heads if num_kv_heads is not None else num_heads
+        self.block_size = block_size
+        self.k_cache = self.v_cache = torch.tensor([])
+
+    def forward(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> torch.Tensor:
+        context = get_context()
+        k_cache, v_cache = self.k_cache, self.v_cache
+        if k_cache.numel() > 0 and v_cache.numel() > 0 and context.slot_mapping is not None:
+            store_kvcache(k.reshape(-1, self.num_kv_heads, self.head_dim),
+                          v.reshape(-1, self.num_kv_heads, self.head_dim),
+                          k_cache, v_cache, context.slot_mapping, self.block_size)
+        if not context.is_verify:
+            raise ValueError("naivllm_amd.Attention serves the verify round only (context.is_verify)")
+        scale = self.scale / (self.head_dim ** 0.5)
+        max_q_len = max(context.seqlens_q)
+        block_m = max(16, 1 << (max_q_len - 1).bit_length())
+        q = q.reshape(-1, self.num_heads, self.head_dim)
+        o = paged_attention_verify(
+            q, k_cache, v_cache, context.block_tables, context.context_lens, context.cu_seqlens_q,
+            context.positions, scale, self.num_heads, self.num_kv_heads, self.head_dim, self.block_size,
+            block_m, max_q_len=max_q_len)
+        return o.reshape(o.shape[0], self.num_heads * self.head_dim)

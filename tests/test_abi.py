@@ -1,0 +1,78 @@
+"""The C ABI library loads, exports every symbol include/naivspec.h
+declares, and rejects bad arguments with the documented codes — all
+without touching a GPU (argument checks run before any launch)."""
+
+import os
+import re
+
+import pytest
+
+from naivllm_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "naivspec.h")
+
+
+def header_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"\b(nsv_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    h = _lib.lib()
+    syms = header_symbols()
+    assert syms, "no declarations found"
+    for name in syms:
+        assert hasattr(h, name), f"{name} declared in naivspec.h but not exported"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+
+
+def test_version_and_error_strings():
+    h = _lib.lib()
+    assert h.nsv_version() >= 100
+    assert h.nsv_error_string(0) == b"ok"
+    assert h.nsv_error_string(-1) == b"invalid argument"
+    assert h.nsv_error_string(-2) == b"unsupported shape"
+    assert h.nsv_error_string(-3) == b"workspace missing or too small"
+
+
+def test_verify_attention_rejects_bad_shapes_before_launch():
+    h = _lib.lib()
+    base = dict(B=8, T=72, H=16, Hkv=8, D=128, bs=256, mb=6, mq=9, dt=1, split=0)
+
+    def call(**kw):
+        a = {**base, **kw}
+        return h.nsv_verify_attention(1, 1, 1, 1, 1, 1, 1, 1, 0.1, a["B"], a["T"], a["H"], a["Hkv"], a["D"], a["bs"],
+                                      a["mb"], a["mq"], a["dt"], a["split"], None, 0, None)
+
+    assert call(D=96) == -2          # head_dim outside {64, 128}
+    assert call(H=12, Hkv=8) == -2   # heads not a multiple of kv heads
+    assert call(bs=100) == -2        # page size not a power of two
+    assert call(H=64, Hkv=8) == -2   # GQA group x query rows > 64
+    assert call(dt=7) == -1
+    assert call(split=100) == -1     # split not a multiple of 128
+    assert call(B=-1) == -1
+    assert call() == -3              # needs a workspace for 6 splits
+    assert call(B=0) == 0 and call(T=0) == 0
+
+
+def test_workspace_size_matches_split_plan():
+    h = _lib.lib()
+    # config 2: 6 pages x 256 keys, auto split 128 -> 12 splits of 18 rows x (128 + 2) floats
+    assert h.nsv_verify_attention_workspace_size(8, 16, 8, 128, 256, 6, 9, 1, 0) == 8 * 8 * 12 * 18 * 130 * 4
+    # one split: no workspace
+    assert h.nsv_verify_attention_workspace_size(1, 16, 8, 128, 256, 1, 9, 1, 256) == 0
+
+
+def test_store_kv_rejects_bad_arguments():
+    h = _lib.lib()
+    assert h.nsv_store_kv(1, 1, 1, 1, 1, 4, 8, 128, 16, 5, None) == -1
+    assert h.nsv_store_kv(None, 1, 1, 1, 1, 4, 8, 128, 16, 1, None) == -1
+    assert h.nsv_store_kv(1, 1, 1, 1, 1, 4, 1, 4, 16, 1, None) == -2   # 8-byte rows
+    assert h.nsv_store_kv(1, 1, 1, 1, 1, 0, 8, 128, 16, 1, None) == 0
+
+
+def test_wrappers_raise_value_error_on_rejected_arguments():
+    with pytest.raises(ValueError):
+        _lib.check(-2, "op")
+    with pytest.raises(_lib.NaivspecError):
+        _lib.check(1, "op")
