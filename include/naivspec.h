@@ -58,7 +58,13 @@ const char* nsv_error_string(int code);
  *   max_q_len     >= every cu_seqlens_q[b+1]-cu_seqlens_q[b] (host-known,
  *                 as the reference computes block_m from seqlens_q)
  *   kv_split_tokens  keys per workgroup split (multiple of 128); 0 = auto
- * Supported: D in {64, 128}; H % Hkv == 0; (H/Hkv)*max_q_len <= 64.
+ * Supported: D in {64, 128}; H % Hkv == 0; (H/Hkv)*max_q_len <= 64;
+ * block_size a power of two.
+ * Workspace: nsv_verify_attention_workspace_size() bytes (0 when every
+ * sequence fits one split) of fp32 split partials, no initialisation
+ * needed; calls that share a workspace must not run concurrently.  A call
+ * is one kernel, or two when some sequence spans several key splits (the
+ * second merges the splits).
  */
 size_t nsv_verify_attention_workspace_size(int B, int H, int Hkv, int D,
                                            int block_size, int max_blocks,

@@ -84,3 +84,22 @@ def stream_ptr(device: torch.device) -> int:
 
 def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
+
+
+_workspaces: dict = {}
+
+
+def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
+    """Per-device scratch buffer for the kernels' split partials, grown on
+    demand and reused by every call on the device (so calls must be ordered
+    on one stream, as torch's current stream orders them)."""
+    if nbytes <= 0:
+        return None
+    key = (device.type, device.index if device.index is not None else torch.cuda.current_device())
+    buf = _workspaces.get(key)
+    if buf is None or buf.numel() < nbytes:
+        size = max(nbytes, 2 * (buf.numel() if buf is not None else 0))
+        size = (size + 255) // 256 * 256
+        buf = torch.empty(size, dtype=torch.uint8, device=device)
+        _workspaces[key] = buf
+    return buf

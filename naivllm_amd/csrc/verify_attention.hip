@@ -14,16 +14,27 @@
 //     B operand of O^T = V^T P^T (no register shuffles between the two
 //     products); V is staged through LDS once per 32-key tile and read back
 //     transposed;
-//   * splits of a long context produce fp32 partials (unnormalised O plus
-//     log2-domain max and sum) that a second kernel merges; a sequence that
-//     fits in one split is normalised and written directly.
+//   * a tile's page ids are read once (one lane per key) and broadcast with
+//     lane shuffles, the next tile's ids are prefetched, and every K/V load
+//     is unconditional (masked keys read a valid dummy row), so all loads of
+//     a tile are in flight together;
+//   * the four waves of a workgroup take interleaved 32-key tiles and merge
+//     their (max, sum, O) through LDS at the end with one float4 write per
+//     element and a single barrier;
+//   * splits of a long context write fp32 partials (unnormalised O plus
+//     log2-domain max and sum) that a second kernel merges — the kernel
+//     boundary is what makes them visible across XCDs, at a fraction of the
+//     cost of device-scope fences, which write back and invalidate the whole
+//     L2 of every XCD that executes one.  A sequence that fits one split is
+//     normalised and written directly by the first kernel.
 
 #include "common.h"
 
 namespace {
 
-constexpr int kTile = 32;        // keys per wave iteration
-constexpr int kWaves = 4;        // waves per workgroup (bf16 path)
+constexpr int kTile = 32;   // keys per wave iteration
+constexpr int kBf16Waves = 8;  // waves per workgroup (bf16 path)
+constexpr int kMaxSplitPages = 1024;  // block-table entries of one split staged in LDS
 constexpr float kNegInf = -__builtin_inff();
 
 struct VerifyArgs {
@@ -35,19 +46,16 @@ struct VerifyArgs {
   const int32_t* cu_seqlens_q;
   const int64_t* positions;
   void* out;
-  float* part_o;   // [B, Hkv, S, Mv, D]  unnormalised split outputs
-  float* part_ml;  // [B, Hkv, S, Mv, 2]  (running max, running sum), log2 domain
+  float* part_ml;    // [B, Hkv, S, Mv, 2]  (running max, running sum), log2 domain
+  float* part_o;     // [B, Hkv, S, Mv, D]  unnormalised split outputs
   float scale_log2;  // softmax scale * log2(e)
-  int H, Hkv, G, bs_log2, max_blocks, QL, Mv, S, split_tokens;
+  int H, Hkv, G, bs_log2, max_blocks, QL, Mv, S, split_tokens, P8, npairs;
+  int dqc;           // head-dim slices per pair (bf16 path)
 };
 
-__device__ __forceinline__ u32x4 load16(const void* p) {
-  return *reinterpret_cast<const u32x4*>(p);
-}
+__device__ __forceinline__ u32x4 load16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 
-__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) {
-  return __builtin_bit_cast(bf16x8, v);
-}
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 // Keys of sequence b the kernels visit: never past the block table's width,
 // the bound the reference's chunk loop has (layers/attention.py:572).
@@ -63,61 +71,149 @@ __device__ __forceinline__ int splits_for(int ctx, int split_tokens) {
   return ctx <= split_tokens ? 1 : (ctx + split_tokens - 1) / split_tokens;
 }
 
+// Workgroup -> (split, pair) with every split of a (sequence, kv-head) pair
+// on the same XCD (workgroups are dealt to the 8 XCDs round-robin), so the
+// pair's shared query rows and partials stay in one L2.
+__device__ __forceinline__ void decode_block(const VerifyArgs& a, int& split, int& pair) {
+  const int i = blockIdx.x;
+  const int y = i >> 3;
+  split = y / a.P8;
+  pair = (y - split * a.P8) * 8 + (i & 7);
+}
+
 // ---------------------------------------------------------------------------
 // bf16 path: 4 waves, MFMA 16x16x32.
 // ---------------------------------------------------------------------------
-template <int MT, int DH>
-__global__ __launch_bounds__(256, 2) void verify_attn_bf16_kernel(VerifyArgs a) {
-  constexpr int KS = DH / 32;           // k-steps of S^T = K Q^T
-  constexpr int DT = DH / 16;           // 16-wide d tiles of O^T
-  constexpr int MP = MT * 16;           // padded query rows
-  constexpr int VSTR = DH + 4;          // staged V row stride (bf16); 8-byte aligned and
-                                        // bank-conflict free for the transposed reads
-  constexpr int VCH = DH / 8;           // 16-byte chunks per V row
-  constexpr int VLOADS = kTile * VCH / NSV_WAVE;
-  constexpr int OSTR = DH + 1;
+// Cross-lane reductions over the four lanes c, c+16, c+32, c+48 that hold one
+// query row's statistics, with gfx950's permlane swaps (VALU, no LDS round
+// trip): permlane{16,32}_swap(x, x) returns {x[l], x[l ^ 16 or 32]}.
+__device__ __forceinline__ float row_max4(float v) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
+__device__ __forceinline__ float row_sum4(float v) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
 
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds[kWaves][kTile * VSTR];
-  __shared__ float red_m[kWaves][MP];
-  __shared__ float red_l[kWaves][MP];
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+// gfx950 transposing LDS read: within each 16-lane group, lane i receives
+// element (i % 4) of the 4-element rows addressed by lanes 4j + i/4, j = 0..3.
+__device__ __forceinline__ uint2 lds_read_tr(const uint16_t* p) {
+  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+  return __builtin_bit_cast(uint2, v);
+}
+
+// Workgroup = (pair, slice dq of DC head dims, key split); its kBf16Waves
+// waves take interleaved 32-key tiles of the split.  Every slice recomputes
+// the scores (cheap: the kernel is HBM bound) and reads the pair's K from
+// the L2 its sibling slices share (all workgroups of a pair sit on one XCD),
+// so HBM sees each K/V byte about once while the grid has 128/DC times more
+// workgroups than pairs — enough to cover the chip without key splits in
+// the common case, which keeps the operator a single kernel.
+//
+// Each wave runs a two-stage register pipeline: tile i+1's K and V loads
+// are in flight while tile i computes; two waves share each SIMD.  Block-
+// table entries of the split are staged in LDS once.  UPAGE (block_size
+// >= 32): a tile lies in one page, whose id is wave-uniform (scalar base
+// address, 32-bit offsets).
+//
+// Softmax runs on raw scores: the running max m is taken over q.k, and
+// p = 2^(q.k * scale*log2e - m * scale*log2e) is one FMA plus the hardware
+// exp2 (results below 2^-126 flush to zero; their weight is negligible, as
+// with the flush-to-zero exp of the reference's Triton kernel).  Tiles with
+// every key present and below every real query row's position skip masking.
+template <int MT, int DH, int DC, bool UPAGE>
+__global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(VerifyArgs a) {
+  constexpr int NW = kBf16Waves;
+  constexpr int NT = NW * 64;
+  constexpr int KS = DH / 32;    // k-steps of S^T = K Q^T
+  constexpr int DT = DC / 16;    // 16-wide d tiles of this slice
+  constexpr int MP = MT * 16;    // padded query rows
+  constexpr int VCH = DC / 8;    // 16-byte chunks per key in the slice
+  constexpr int VL = kTile * VCH / NSV_WAVE;  // 16-byte V loads per lane per tile
+  constexpr int VSTR = DC + 16;  // staged V row stride (bf16): an odd multiple of 32 bytes,
+                                 // so the transposing reads of 8 rows hit distinct banks
+  constexpr int RSTR = DC + 4;   // merge-region row stride (floats)
+  constexpr int STAGE = NW * kTile * VSTR * 2;
+  constexpr int MTILE_BYTES = NW * 16 * RSTR * 4;  // one m-tile of every wave's O
+  constexpr int MTP0 = (72 * 1024) / MTILE_BYTES;
+  constexpr int MTP = MTP0 < 1 ? 1 : (MTP0 > MT ? MT : MTP0);  // m-tiles merged per pass
+  constexpr int MERGE = MTP * MTILE_BYTES;
+  constexpr int SMEM = STAGE > MERGE ? STAGE : MERGE;
+
+  __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM];
+  __shared__ int pages[kMaxSplitPages];
+  __shared__ float red_m[NW][MP];
+  __shared__ float red_l[NW][MP];
   __shared__ float row_l[MP];
   __shared__ float row_ms[MP];
-  __shared__ float red_o[MP * OSTR];
+  __shared__ int row_pos[MP];
 
-  const int split = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // ---- workgroup -> (pair, dq, split); every workgroup of a pair on one XCD
+  const int wg = blockIdx.x;
+  const int yy = wg >> 3;
+  const int pair = (yy % a.P8) * 8 + (wg & 7);
+  const int rest = yy / a.P8;
+  const int dq = rest % a.dqc, split = rest / a.dqc;
+  if (pair >= a.npairs) return;  // grid rounds the pair count up to a multiple of 8
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g4 = lane >> 4, c = lane & 15;
-
-  const int ctx = context_len(a, b);
-  const int nsplit = splits_for(ctx, a.split_tokens);
-  if (split >= nsplit) return;  // uniform per workgroup
+  const int b = pair / a.Hkv, hk = pair - b * a.Hkv;
+  const int max_ctx = a.max_blocks << a.bs_log2;
   const int tok_begin = split * a.split_tokens;
-  const int tok_end = min(ctx, tok_begin + a.split_tokens);
+  const int range_end = min(max_ctx, tok_begin + a.split_tokens);
+  if (tok_begin >= max_ctx) return;
+
+  // ---- independent loads first: the split's block-table slice (into LDS),
+  // context length and query-row range; then Q and positions.
+  const int pg0 = tok_begin >> a.bs_log2;
+  const int npg = ((range_end - 1) >> a.bs_log2) - pg0 + 1;
+  {
+    const int32_t* btrow = a.block_tables + (int64_t)b * a.max_blocks + pg0;
+    for (int j = tid; j < npg; j += NT) pages[j] = btrow[j];
+  }
+  const int ctx = context_len(a, b);
   const int q0 = a.cu_seqlens_q[b];
   const int qlen = a.cu_seqlens_q[b + 1] - q0;
+  const int nsplit = splits_for(ctx, a.split_tokens);
+  if (split >= nsplit) return;  // uniform per workgroup
+  const int tok_end = min(ctx, range_end);
 
   // Q^T as the B operand: lane (g4, c) holds row m = 16*mt + c, dims 32*ks + 8*g4 .. +7.
+  // Rows outside the sequence read row 0 and keep position -1; rows at a
+  // negative position (outside the sequence or inert padding) are written
+  // as zeros, whatever they accumulated.
   bf16x8 qB[MT][KS];
   int qpos[MT];
-  const u32x4 zero4 = {0u, 0u, 0u, 0u};
+  int qmin = 0x7fffffff;  // lowest real query position of this lane's rows
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int m = mt * 16 + c;
     const int g = m / a.QL, t = m - g * a.QL;
     const bool ok = (m < a.Mv) && (t < qlen);
-    int pos = -1;
-    const bf16_t* qrow = nullptr;
-    if (ok) {
-      pos = (int)a.positions[q0 + t];
-      qrow = (const bf16_t*)a.q + ((int64_t)(q0 + t) * a.H + hk * a.G + g) * DH;
-    }
-    qpos[mt] = pos;
+    const int row = ok ? q0 + t : 0;
+    const int gg = ok ? g : 0;
+    const int pos = (int)a.positions[row];
+    qpos[mt] = ok ? pos : -1;
+    if (qpos[mt] >= 0) qmin = min(qmin, qpos[mt]);
+    if (w == 0 && g4 == 0) row_pos[m] = qpos[mt];
+    const bf16_t* qrow = (const bf16_t*)a.q + ((int64_t)row * a.H + hk * a.G + gg) * DH;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks)
-      qB[mt][ks] = as_bf16x8(ok ? load16(qrow + ks * 32 + g4 * 8) : zero4);
+    for (int ks = 0; ks < KS; ++ks) qB[mt][ks] = as_bf16x8(load16(qrow + ks * 32 + g4 * 8));
   }
+#pragma unroll
+  for (int o = 1; o < 16; o <<= 1) qmin = min(qmin, __shfl_xor(qmin, o, NSV_WAVE));
+  qmin = __builtin_amdgcn_readfirstlane(qmin);
 
-  float m_run[MT], l_run[MT];
+  float m_run[MT], l_run[MT];  // running max of raw scores, running sum
   f32x4 acc[DT][MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
@@ -127,144 +223,194 @@ __global__ __launch_bounds__(256, 2) void verify_attn_bf16_kernel(VerifyArgs a) 
     for (int dt = 0; dt < DT; ++dt) acc[dt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  const int32_t* bt = a.block_tables + (int64_t)b * a.max_blocks;
+  const float sc = a.scale_log2;
   const int bs_mask = (1 << a.bs_log2) - 1;
-  const int64_t tok_stride = (int64_t)a.Hkv * DH;
+  const int tok_stride = a.Hkv * DH;  // elements between consecutive keys of a page
+  const int64_t page_elems = (int64_t)tok_stride << a.bs_log2;
   const bf16_t* kbase = (const bf16_t*)a.k_cache + hk * DH;
-  const bf16_t* vbase = (const bf16_t*)a.v_cache + hk * DH;
-  uint16_t* vl = v_lds[w];
+  const bf16_t* vbase = (const bf16_t*)a.v_cache + hk * DH + dq * DC;
+  uint16_t* vl = reinterpret_cast<uint16_t*>(smem) + w * kTile * VSTR;
+  __syncthreads();  // block-table slice visible
 
   const int ntiles = (tok_end - tok_begin + kTile - 1) / kTile;
-  const int niter = (ntiles + kWaves - 1) / kWaves;  // same trip count in every wave
+  const int niter = (ntiles + NW - 1) / NW;  // same trip count in every wave
 
-  for (int it = 0; it < niter; ++it) {
-    const int n0 = tok_begin + (it * kWaves + w) * kTile;
+  struct Tile {
+    u32x4 k[2][KS];  // K as the A operand: lane (g4, c) holds key 16*t + c, dims 32*ks + 8*g4 .. +7
+    u32x4 v[VL];     // V slice rows, coalesced: chunk j*64 + lane = (key, 16-byte chunk)
+    uint64_t kmask;  // keys of the tile that exist (inside the split, page mapped)
+    int n0;
+    int nvalid;      // UPAGE: the existing keys are exactly the first nvalid of the tile
+  };
 
-    // Which of the tile's 32 keys exist (inside the split, page mapped).
-    bool key_ok = false;
-    if (lane < kTile) {
-      const int n = n0 + lane;
-      if (n < tok_end) key_ok = bt[n >> a.bs_log2] >= 0;
-    }
-    const uint64_t kmask = __ballot(key_ok);
-
-    // K as the A operand: lane (g4, c) holds key 16*t + c, dims 32*ks + 8*g4 .. +7.
-    u32x4 kraw[2][KS];
+  // Issue every load of wave-tile `it`.  Masked keys read the row of a key
+  // that exists (finite data, zero weight), or any mapped row when none does.
+  auto issue = [&](Tile& T, int it) {
+    T.n0 = tok_begin + (it * NW + w) * kTile;
+    if constexpr (UPAGE) {
+      int nvalid = min(max(tok_end - T.n0, 0), kTile);
+      int pg = nvalid > 0 ? pages[(T.n0 >> a.bs_log2) - pg0] : -1;
+      pg = __builtin_amdgcn_readfirstlane(pg);
+      if (pg < 0) nvalid = 0;
+      T.nvalid = nvalid;
+      T.kmask = nvalid >= kTile ? 0xffffffffull : ((1ull << nvalid) - 1);
+      // byte addressing: scalar page base + 32-bit lane offsets
+      const size_t page_off = (size_t)(pg < 0 ? 0 : pg) * (size_t)page_elems * 2;
+      const char* kp = (const char*)kbase + page_off;
+      const char* vp = (const char*)vbase + page_off;
+      const unsigned base_key = (unsigned)(T.n0 & bs_mask);
+      const unsigned row_bytes = (unsigned)tok_stride * 2;
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const int nr = t * 16 + c;
-      const bool ok = (kmask >> nr) & 1;
-      const bf16_t* kp = nullptr;
-      if (ok) {
-        const int n = n0 + nr;
-        kp = kbase + ((int64_t)bt[n >> a.bs_log2] * (bs_mask + 1) + (n & bs_mask)) * tok_stride;
+      for (int t = 0; t < 2; ++t) {
+        const int r = t * 16 + c;
+        const unsigned off = (base_key + (r < nvalid ? r : 0)) * row_bytes + g4 * 16;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) T.k[t][ks] = load16(kp + off + ks * 64);
       }
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) kraw[t][ks] = ok ? load16(kp + ks * 32 + g4 * 8) : zero4;
-    }
-    // V rows, coalesced: 64 lanes cover 64 * 16 bytes = 4 (DH=128) key rows per load.
-    u32x4 vraw[VLOADS];
+      for (int j = 0; j < VL; ++j) {
+        const int id = j * NSV_WAVE + lane;
+        const int r = id / VCH, ch = id - r * VCH;
+        const unsigned off = (base_key + (r < nvalid ? r : 0)) * row_bytes + ch * 16;
+        T.v[j] = load16(vp + off);
+      }
+    } else {
+      const int n = T.n0 + lane;
+      const int pg = (lane < kTile && n < tok_end) ? pages[(n >> a.bs_log2) - pg0] : -1;
+      T.kmask = __ballot(pg >= 0);
+      T.nvalid = 0;
+      const int first = T.kmask ? __builtin_ctzll(T.kmask) : 0;
+      const int pg_first = __shfl(pg, first, NSV_WAVE);
+      const int64_t dflt = T.kmask ? (int64_t)pg_first * page_elems + (int64_t)((T.n0 + first) & bs_mask) * tok_stride
+                                   : 0;
 #pragma unroll
-    for (int r = 0; r < VLOADS; ++r) {
-      const int idx = r * NSV_WAVE + lane;
-      const int tk = idx / VCH, dc = idx - tk * VCH;
-      const bool ok = (kmask >> tk) & 1;
-      vraw[r] = zero4;
-      if (ok) {
-        const int n = n0 + tk;
-        vraw[r] = load16(vbase + ((int64_t)bt[n >> a.bs_log2] * (bs_mask + 1) + (n & bs_mask)) * tok_stride +
-                         dc * 8);
+      for (int t = 0; t < 2; ++t) {
+        const int r = t * 16 + c;
+        const int pk = __shfl(pg, r, NSV_WAVE);
+        const int64_t row = ((T.kmask >> r) & 1) ? (int64_t)pk * page_elems + (int64_t)((T.n0 + r) & bs_mask) * tok_stride
+                                                 : dflt;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) T.k[t][ks] = load16(kbase + row + g4 * 8 + ks * 32);
+      }
+#pragma unroll
+      for (int j = 0; j < VL; ++j) {
+        const int id = j * NSV_WAVE + lane;
+        const int r = id / VCH, ch = id - r * VCH;
+        const int pv = __shfl(pg, r, NSV_WAVE);
+        const int64_t row = ((T.kmask >> r) & 1) ? (int64_t)pv * page_elems + (int64_t)((T.n0 + r) & bs_mask) * tok_stride
+                                                 : dflt;
+        T.v[j] = load16(vbase + row + ch * 8);
       }
     }
+  };
 
+  auto compute = [&](const Tile& T) {
+    if (T.kmask == 0) return;  // uniform: nothing of this tile exists
     // S^T tile: lane (g4, c), element i -> key 16*t + 4*g4 + i, query row 16*mt + c.
     f32x4 sacc[2][MT];
 #pragma unroll
     for (int t = 0; t < 2; ++t)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        f32x4 s = {0.f, 0.f, 0.f, 0.f};
+        f32x4 sv = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
-          s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kraw[t][ks]), qB[mt][ks], s, 0, 0, 0);
-        sacc[t][mt] = s;
+          sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(T.k[t][ks]), qB[mt][ks], sv, 0, 0, 0);
+        sacc[t][mt] = sv;
       }
-
-    // Online softmax in the log2 domain; every row's statistics are held
-    // redundantly by the four lanes that share its column c.
+    // Stage the V slice (this wave's private LDS rows; LDS ops of one wave
+    // complete in order).
+#pragma unroll
+    for (int j = 0; j < VL; ++j) {
+      const int id = j * NSV_WAVE + lane;
+      const int r = id / VCH, ch = id - r * VCH;
+      *reinterpret_cast<u32x4*>(vl + r * VSTR + ch * 8) = T.v[j];
+    }
+    // Masked keys get -inf before any arithmetic (exact 0 weight).  Only the
+    // tiles at a split's end or across a query row's position need it.
+    const bool full = (T.kmask == 0xffffffffull) && (T.n0 + kTile - 1 <= qmin);
+    if (!full) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = t * 16 + g4 * 4 + i;
+          const bool exists = UPAGE ? (r < T.nvalid) : (bool)((T.kmask >> r) & 1);
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+            sacc[t][mt][i] = (exists && T.n0 + r <= qpos[mt]) ? sacc[t][mt][i] : kNegInf;
+        }
+    }
     bf16x8 pB[MT];
+    float alpha[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      float x[2][4];
-      float mx = kNegInf;
-#pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int nr = t * 16 + g4 * 4 + i;
-          const bool ok = ((kmask >> nr) & 1) && (n0 + nr <= qpos[mt]);
-          x[t][i] = ok ? sacc[t][mt][i] * a.scale_log2 : kNegInf;
-          mx = fmaxf(mx, x[t][i]);
-        }
-      mx = fmaxf(mx, __shfl_xor(mx, 16, NSV_WAVE));
-      mx = fmaxf(mx, __shfl_xor(mx, 32, NSV_WAVE));
+      float mx = __builtin_fmaxf(__builtin_fmaxf(sacc[0][mt][0], sacc[0][mt][1]), sacc[0][mt][2]);
+      mx = __builtin_fmaxf(__builtin_fmaxf(mx, sacc[0][mt][3]), sacc[1][mt][0]);
+      mx = __builtin_fmaxf(__builtin_fmaxf(mx, sacc[1][mt][1]), sacc[1][mt][2]);
+      mx = __builtin_fmaxf(mx, sacc[1][mt][3]);
+      mx = row_max4(mx);
       const float m_new = fmaxf(m_run[mt], mx);
-      const float ms = (m_new == kNegInf) ? 0.f : m_new;
-      const float alpha = exp2f(m_run[mt] - ms);
-      float sum = 0.f;
+      const float nb = (m_new == kNegInf) ? 0.f : -m_new * sc;  // exp2 bias
+      alpha[mt] = __builtin_amdgcn_exp2f(fmaf(m_run[mt], sc, nb));
+      float p[2][4];
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float p = exp2f(x[t][i] - ms);
-          x[t][i] = p;
-          sum += p;
-        }
-      sum += __shfl_xor(sum, 16, NSV_WAVE);
-      sum += __shfl_xor(sum, 32, NSV_WAVE);
-      l_run[mt] = l_run[mt] * alpha + sum;
+        for (int i = 0; i < 4; ++i) p[t][i] = __builtin_amdgcn_exp2f(fmaf(sacc[t][mt][i], sc, nb));
+      const float sum = ((p[0][0] + p[0][1]) + (p[0][2] + p[0][3])) + ((p[1][0] + p[1][1]) + (p[1][2] + p[1][3]));
+      l_run[mt] = fmaf(l_run[mt], alpha[mt], row_sum4(sum));
       m_run[mt] = m_new;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) acc[dt][mt] *= alpha;
       // P^T as the B operand of O^T = V^T P^T, rounded to bf16 like the
-      // reference's `p.to(v.dtype)`.  Element j covers key kmap(g4, j).
+      // reference's `p.to(v.dtype)`.  Element j covers key kmap(g4, j) =
+      // 4*g4 + j (j < 4), 16 + 4*g4 + (j - 4) (j >= 4): the keys this lane's
+      // S^T elements hold, so P needs no data movement.
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        pB[mt][i] = (bf16_t)x[0][i];
-        pB[mt][4 + i] = (bf16_t)x[1][i];
+        pB[mt][i] = (bf16_t)p[0][i];
+        pB[mt][4 + i] = (bf16_t)p[1][i];
       }
     }
-
-    // Stage V (this wave's private LDS slice; LDS ops of one wave complete in order).
+    // rescale the accumulators only when some row's running max moved
+    bool moved = false;
 #pragma unroll
-    for (int r = 0; r < VLOADS; ++r) {
-      const int idx = r * NSV_WAVE + lane;
-      const int tk = idx / VCH, dc = idx - tk * VCH;
-      uint2* dst = reinterpret_cast<uint2*>(vl + tk * VSTR + dc * 8);
-      dst[0] = make_uint2(vraw[r].x, vraw[r].y);
-      dst[1] = make_uint2(vraw[r].z, vraw[r].w);
+    for (int mt = 0; mt < MT; ++mt) moved |= alpha[mt] != 1.f;
+    if (__ballot(moved)) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[dt][mt] *= alpha[mt];
     }
     __builtin_amdgcn_wave_barrier();
-
-    // O^T += V^T P^T: lane (g4, c) reads V[kmap(g4, j)][16*dt + c] for j = 0..7,
-    // kmap(g, j) = 4g + j (j < 4), 16 + 4g + (j - 4) (j >= 4) — the keys its S^T
-    // elements hold, so the P operand needs no data movement.
+    // O^T += V^T P^T.  V^T operand of lane (g4, c): V[kmap(g4, j)][16*dt + c];
+    // two transposing reads, each over rows kmap(g4, 4h .. 4h+3) with lane
+    // k = c supplying row 4*g4 (+16 h) + k/4, columns 16*dt + 4*(k%4) .. +3.
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
-      const uint16_t* col = vl + dt * 16 + c;
-      uint32_t v01 = (uint32_t)col[(g4 * 4 + 0) * VSTR] | ((uint32_t)col[(g4 * 4 + 1) * VSTR] << 16);
-      uint32_t v23 = (uint32_t)col[(g4 * 4 + 2) * VSTR] | ((uint32_t)col[(g4 * 4 + 3) * VSTR] << 16);
-      uint32_t v45 = (uint32_t)col[(16 + g4 * 4 + 0) * VSTR] | ((uint32_t)col[(16 + g4 * 4 + 1) * VSTR] << 16);
-      uint32_t v67 = (uint32_t)col[(16 + g4 * 4 + 2) * VSTR] | ((uint32_t)col[(16 + g4 * 4 + 3) * VSTR] << 16);
-      const bf16x8 vA = as_bf16x8(u32x4{v01, v23, v45, v67});
+      const uint16_t* src = vl + (g4 * 4 + (c >> 2)) * VSTR + dt * 16 + (c & 3) * 4;
+      const uint2 lo = lds_read_tr(src);
+      const uint2 hi = lds_read_tr(src + 16 * VSTR);
+      const bf16x8 vA = as_bf16x8(u32x4{lo.x, lo.y, hi.x, hi.y});
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
         acc[dt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vA, pB[mt], acc[dt][mt], 0, 0, 0);
     }
     __builtin_amdgcn_wave_barrier();
+  };
+
+  // ---- two-stage pipeline over this wave's tiles
+  Tile A, B;
+  issue(A, 0);
+  for (int it = 0; it < niter; it += 2) {
+    issue(B, it + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(A);
+    issue(A, it + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(B);
   }
 
-  // ---- merge the four waves' (max, sum, O) ---------------------------------
+  // ---- merge the waves' (max, sum, O) ---------------------------------------
   if (g4 == 0) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
@@ -272,63 +418,66 @@ __global__ __launch_bounds__(256, 2) void verify_attn_bf16_kernel(VerifyArgs a) 
       red_l[w][mt * 16 + c] = l_run[mt];
     }
   }
-  __syncthreads();
+  __syncthreads();  // also: every wave is done with its V staging rows
   if (tid < MP) {
     float M = kNegInf;
 #pragma unroll
-    for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, red_m[ww][tid]);
-    const float ms = (M == kNegInf) ? 0.f : M;
+    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, red_m[ww][tid]);
+    const float ref = (M == kNegInf) ? 0.f : M;
     float L = 0.f;
 #pragma unroll
-    for (int ww = 0; ww < kWaves; ++ww) L += red_l[ww][tid] * exp2f(red_m[ww][tid] - ms);
-    row_ms[tid] = M;
+    for (int ww = 0; ww < NW; ++ww) L += red_l[ww][tid] * __builtin_amdgcn_exp2f((red_m[ww][tid] - ref) * sc);
+    row_ms[tid] = M == kNegInf ? kNegInf : M * sc;  // partials carry the log2-domain max
     row_l[tid] = L;
   }
+  float fac[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int m = mt * 16 + c;
     float M = kNegInf;
 #pragma unroll
-    for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, red_m[ww][m]);
-    const float fac = exp2f(m_run[mt] - ((M == kNegInf) ? 0.f : M));
-#pragma unroll
-    for (int dt = 0; dt < DT; ++dt) acc[dt][mt] *= fac;
+    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, red_m[ww][m]);
+    fac[mt] = __builtin_amdgcn_exp2f((m_run[mt] - ((M == kNegInf) ? 0.f : M)) * sc);
   }
-  for (int ww = 0; ww < kWaves; ++ww) {
-    if (w == ww) {
+  float* region = reinterpret_cast<float*>(smem);  // [NW][MTP * 16][RSTR]
+  constexpr int C4 = DC / 4;
+  const int64_t pbase = ((int64_t)pair * a.S + split) * a.Mv;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+  for (int mp = 0; mp < MT; mp += MTP) {
+    if (mp > 0) __syncthreads();  // previous pass fully read
+    // lane (g4, c) element i of tile (dt, mt) is O[16*mt + c][16*dt + 4*g4 + i]
 #pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
+    for (int mt = mp; mt < mp + MTP && mt < MT; ++mt)
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            float* o = &red_o[(mt * 16 + c) * OSTR + dt * 16 + g4 * 4 + i];
-            *o = (ww == 0 ? 0.f : *o) + acc[dt][mt][i];
-          }
-    }
+      for (int dt = 0; dt < DT; ++dt)
+        *reinterpret_cast<f32x4*>(&region[(w * MTP * 16 + (mt - mp) * 16 + c) * RSTR + dt * 16 + g4 * 4]) =
+            acc[dt][mt] * fac[mt];
     __syncthreads();
+    for (int qd = tid; qd < MTP * 16 * C4; qd += NT) {
+      const int r = qd / C4, c4 = qd - r * C4;
+      const int m = mp * 16 + r;
+      if (m >= a.Mv) continue;
+      f32x4 o = *reinterpret_cast<const f32x4*>(&region[r * RSTR + c4 * 4]);
+#pragma unroll
+      for (int ww = 1; ww < NW; ++ww) o += *reinterpret_cast<const f32x4*>(&region[(ww * MTP * 16 + r) * RSTR + c4 * 4]);
+      if (nsplit == 1) {
+        const int g = m / a.QL, t = m - g * a.QL;
+        if (t >= qlen) continue;
+        const float L = row_l[m];
+        const float inv = (L > 0.f && row_pos[m] >= 0) ? 1.f / L : 0.f;
+        bf16_t* dst = (bf16_t*)a.out + ((int64_t)(q0 + t) * a.H + hk * a.G + g) * DH + dq * DC + c4 * 4;
+        const uint32_t lo = (uint32_t)f32_to_bf16_bits(o[0] * inv) | ((uint32_t)f32_to_bf16_bits(o[1] * inv) << 16);
+        const uint32_t hi = (uint32_t)f32_to_bf16_bits(o[2] * inv) | ((uint32_t)f32_to_bf16_bits(o[3] * inv) << 16);
+        *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+      } else {
+        if (row_pos[m] < 0) o = f32x4{0.f, 0.f, 0.f, 0.f};
+        *reinterpret_cast<f32x4*>(&a.part_o[(pbase + m) * DH + dq * DC + c4 * 4]) = o;
+      }
+    }
   }
-
-  if (nsplit == 1) {
-    bf16_t* out = (bf16_t*)a.out;
-    for (int idx = tid; idx < a.Mv * DH; idx += 256) {
-      const int m = idx / DH, d = idx - m * DH;
-      const int g = m / a.QL, t = m - g * a.QL;
-      if (t >= qlen) continue;
-      const float L = row_l[m];
-      const float v = L > 0.f ? red_o[m * OSTR + d] / L : 0.f;
-      out[((int64_t)(q0 + t) * a.H + hk * a.G + g) * DH + d] = (bf16_t)v;
-    }
-  } else {
-    const int64_t base = (((int64_t)b * a.Hkv + hk) * a.S + split) * a.Mv;
-    for (int idx = tid; idx < a.Mv * DH; idx += 256) {
-      const int m = idx / DH, d = idx - m * DH;
-      a.part_o[(base + m) * DH + d] = red_o[m * OSTR + d];
-    }
-    if (tid < a.Mv) {
-      a.part_ml[(base + tid) * 2 + 0] = row_ms[tid];
-      a.part_ml[(base + tid) * 2 + 1] = row_l[tid];
-    }
+  if (nsplit > 1 && dq == 0 && tid < a.Mv) {
+    a.part_ml[(pbase + tid) * 2 + 0] = row_pos[tid] >= 0 ? row_ms[tid] : kNegInf;
+    a.part_ml[(pbase + tid) * 2 + 1] = row_pos[tid] >= 0 ? row_l[tid] : 0.f;
   }
 }
 
@@ -344,8 +493,11 @@ __global__ __launch_bounds__(64) void verify_attn_f32_kernel(VerifyArgs a) {
   __shared__ float p_s[MP][NSV_WAVE];
   __shared__ int pos_s[MP];
 
-  const int split = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+  int split, pair;
+  decode_block(a, split, pair);
+  if (pair >= a.npairs) return;
   const int lane = threadIdx.x;
+  const int b = pair / a.Hkv, hk = pair - b * a.Hkv;
   const int ctx = context_len(a, b);
   const int nsplit = splits_for(ctx, a.split_tokens);
   if (split >= nsplit) return;
@@ -449,48 +601,66 @@ __global__ __launch_bounds__(64) void verify_attn_f32_kernel(VerifyArgs a) {
         out[((int64_t)(q0 + t) * a.H + hk * a.G + g) * DH + lane + 64 * e] =
             l_run[m] > 0.f ? acc[m][e] / l_run[m] : 0.f;
     }
-  } else {
-    const int64_t base = (((int64_t)b * a.Hkv + hk) * a.S + split) * a.Mv;
+    return;
+  }
+  const int64_t base = ((int64_t)pair * a.S + split) * a.Mv;
 #pragma unroll
-    for (int m = 0; m < MP; ++m) {
-      if (m >= a.Mv) continue;
+  for (int m = 0; m < MP; ++m) {
+    if (m >= a.Mv) continue;
 #pragma unroll
-      for (int e = 0; e < E; ++e) a.part_o[(base + m) * DH + lane + 64 * e] = acc[m][e];
-      if (lane == 0) {
-        a.part_ml[(base + m) * 2 + 0] = m_run[m];
-        a.part_ml[(base + m) * 2 + 1] = l_run[m];
-      }
+    for (int e = 0; e < E; ++e) a.part_o[(base + m) * DH + lane + 64 * e] = acc[m][e];
+    if (lane == 0) {
+      a.part_ml[(base + m) * 2 + 0] = m_run[m];
+      a.part_ml[(base + m) * 2 + 1] = l_run[m];
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// Split merge: one workgroup per (row, kv-head, sequence), one lane per dim.
+// Split merge: one workgroup per (query row of the group, pair), one lane
+// per head dim.  The splits' (max, sum) pairs are staged in LDS (dynamic,
+// 2 * S floats), then every lane has all of its nsplit partial loads in
+// flight at once.
 // ---------------------------------------------------------------------------
 template <typename OutT>
-__global__ __launch_bounds__(128) void verify_combine_kernel(VerifyArgs a, int DH) {
-  const int m = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
-  const int d = threadIdx.x;
+__global__ __launch_bounds__(128) void verify_merge_kernel(VerifyArgs a, int DH) {
+  extern __shared__ float ml_s[];  // [S][2]
+  __shared__ float stat[2];
+  const int m = blockIdx.x, pair = blockIdx.y;
+  if (pair >= a.npairs) return;
+  const int b = pair / a.Hkv, hk = pair - b * a.Hkv;
   const int ctx = context_len(a, b);
   const int nsplit = splits_for(ctx, a.split_tokens);
   if (nsplit <= 1) return;  // written by the attention kernel itself
-  const int g = m / a.QL, t = m - g * a.QL;
   const int q0 = a.cu_seqlens_q[b];
   const int qlen = a.cu_seqlens_q[b + 1] - q0;
-  if (t >= qlen || d >= DH) return;
-  const int64_t base = (((int64_t)b * a.Hkv + hk) * a.S) * a.Mv + m;
-  float M = kNegInf;
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, a.part_ml[(base + (int64_t)s * a.Mv) * 2]);
-  const float ms = (M == kNegInf) ? 0.f : M;
-  float L = 0.f, o = 0.f;
-  for (int s = 0; s < nsplit; ++s) {
-    const int64_t r = base + (int64_t)s * a.Mv;
-    const float f = exp2f(a.part_ml[r * 2] - ms);
-    L += a.part_ml[r * 2 + 1] * f;
-    o += a.part_o[r * DH + d] * f;
+  const int g = m / a.QL, t = m - g * a.QL;
+  if (t >= qlen) return;
+  const int64_t base = (int64_t)pair * a.S * a.Mv + m;  // row of split 0
+  for (int s = threadIdx.x; s < nsplit; s += blockDim.x) {
+    const float2 v = *reinterpret_cast<const float2*>(&a.part_ml[(base + (int64_t)s * a.Mv) * 2]);
+    ml_s[2 * s] = v.x;
+    ml_s[2 * s + 1] = v.y;
   }
-  const float v = L > 0.f ? o / L : 0.f;
-  ((OutT*)a.out)[((int64_t)(q0 + t) * a.H + hk * a.G + g) * DH + d] = (OutT)v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float M = kNegInf;
+    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, ml_s[2 * s]);
+    const float ref = (M == kNegInf) ? 0.f : M;
+    float L = 0.f;
+    for (int s = 0; s < nsplit; ++s) L += ml_s[2 * s + 1] * exp2f(ml_s[2 * s] - ref);
+    stat[0] = ref;
+    stat[1] = L > 0.f ? 1.f / L : 0.f;
+  }
+  __syncthreads();
+  const int d = threadIdx.x;
+  if (d >= DH) return;
+  const float ref = stat[0];
+  float o = 0.f;
+#pragma unroll 16
+  for (int s = 0; s < nsplit; ++s)
+    o += exp2f(ml_s[2 * s] - ref) * a.part_o[(base + (int64_t)s * a.Mv) * DH + d];
+  ((OutT*)a.out)[((int64_t)(q0 + t) * a.H + hk * a.G + g) * DH + d] = (OutT)(o * stat[1]);
 }
 
 // ---------------------------------------------------------------------------
@@ -513,7 +683,7 @@ __global__ __launch_bounds__(256) void store_kv_kernel(const u32x4* __restrict__
 // Host side.
 // ---------------------------------------------------------------------------
 struct Plan {
-  int G, QL, Mv, MT, split, S;
+  int G, QL, Mv, MT, split, S, dqc;
 };
 
 int ilog2_exact(int v) {
@@ -521,6 +691,18 @@ int ilog2_exact(int v) {
   int l = 0;
   while ((1 << l) < v) ++l;
   return l;
+}
+
+// Compute units of the current device (256 on MI355X); the plan only uses
+// it to size the grid, so a failed query falls back to that figure.
+int device_cus() {
+  int dev = 0, cus = 0;
+  if (hipGetDevice(&dev) != hipSuccess || hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  return cus;
 }
 
 int make_plan(int B, int H, int Hkv, int D, int block_size, int max_blocks, int max_q_len, int dtype,
@@ -537,31 +719,76 @@ int make_plan(int B, int H, int Hkv, int D, int block_size, int max_blocks, int 
   p->MT = (p->Mv + 15) / 16;
   const int64_t max_ctx = (int64_t)max_blocks * block_size;
   if (max_ctx > (int64_t)1 << 30) return NSV_ERR_UNSUPPORTED;
-  int split = kv_split_tokens;
-  if (split < 0 || (split % 128)) return NSV_ERR_ARG;
-  if (split == 0) {
-    // Enough workgroups to cover the chip a few times over, without
-    // letting the fp32 partials grow past a few percent of the KV bytes.
-    const int64_t target = dtype == NSV_BF16 ? 2048 : 1024;
-    split = dtype == NSV_BF16 ? 128 : 256;
-    while ((int64_t)B * Hkv * ((max_ctx + split - 1) / split) > target && split < 8192) split *= 2;
+  if (kv_split_tokens < 0 || (kv_split_tokens % 128)) return NSV_ERR_ARG;
+  const int64_t pairs = (int64_t)B * Hkv;
+  // longest split whose block-table slice fits the kernel's LDS copy
+  const int64_t page_cap = ((int64_t)(kMaxSplitPages - 1) * block_size) / 128 * 128;
+  int64_t split = kv_split_tokens;
+  p->dqc = 1;
+  if (dtype == NSV_BF16) {
+    const int cus = device_cus();
+    // widest head-dim slice whose double-buffered K/V tiles and accumulators
+    // fit the register file without spilling: 64 dims up to 32 padded query
+    // rows, 32 beyond
+    const int dc_max = p->MT <= 2 ? 64 : 32;
+    p->dqc = D > dc_max ? D / dc_max : 1;
+    while (pairs * p->dqc < cus && p->dqc < D / 32) p->dqc *= 2;
+    if (split == 0) {
+      split = (max_ctx + 127) / 128 * 128;  // one split per sequence ...
+      const int64_t units = pairs * p->dqc;
+      if (units > 0 && units < cus) {        // ... unless the grid would leave CUs idle
+        const int64_t want = (cus + units - 1) / units;
+        split = ((max_ctx + want - 1) / want + 127) / 128 * 128;
+      }
+      if (split > page_cap) split = page_cap;
+      if (split < 128) split = 128;
+    } else if (split > page_cap) {
+      return NSV_ERR_UNSUPPORTED;
+    }
+  } else if (split == 0) {
+    // fp32: enough one-wave workgroups to cover the chip a few times over
+    split = 256;
+    while (pairs * ((max_ctx + split - 1) / split) > 1024 && split < 8192) split *= 2;
   }
-  p->split = split;
+  p->split = (int)split;
   p->S = (int)((max_ctx + split - 1) / split);
+  if (p->S > 8192) return NSV_ERR_UNSUPPORTED;  // the merge stages 2 * S floats in LDS
   return NSV_OK;
 }
 
+// Workspace: [part_ml, 256-byte aligned][part_o].
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+size_t ml_bytes(int B, int Hkv, const Plan& p) { return align256((size_t)B * Hkv * p.S * p.Mv * 2 * sizeof(float)); }
+
 size_t workspace_bytes_for(int B, int Hkv, int D, const Plan& p) {
   if (p.S <= 1) return 0;
-  return (size_t)B * Hkv * p.S * p.Mv * (size_t)(D + 2) * sizeof(float);
+  return ml_bytes(B, Hkv, p) + (size_t)B * Hkv * p.S * p.Mv * (size_t)D * sizeof(float);
+}
+
+template <int MT, int DH, int DC>
+void launch_bf16_dc(const VerifyArgs& a, dim3 grid, hipStream_t s) {
+  if (a.bs_log2 >= 5)
+    hipLaunchKernelGGL((verify_attn_bf16_kernel<MT, DH, DC, true>), grid, dim3(kBf16Waves * 64), 0, s, a);
+  else
+    hipLaunchKernelGGL((verify_attn_bf16_kernel<MT, DH, DC, false>), grid, dim3(kBf16Waves * 64), 0, s, a);
 }
 
 template <int MT>
 void launch_bf16(const VerifyArgs& a, int D, dim3 grid, hipStream_t s) {
-  if (D == 128)
-    hipLaunchKernelGGL((verify_attn_bf16_kernel<MT, 128>), grid, dim3(256), 0, s, a);
-  else
-    hipLaunchKernelGGL((verify_attn_bf16_kernel<MT, 64>), grid, dim3(256), 0, s, a);
+  const int dc = D / a.dqc;  // the plan keeps dc at 32, or 64 for MT <= 2
+  if constexpr (MT <= 2) {
+    if (D == 128) {
+      if (dc == 32) launch_bf16_dc<MT, 128, 32>(a, grid, s);
+      else launch_bf16_dc<MT, 128, 64>(a, grid, s);
+    } else {
+      if (dc == 32) launch_bf16_dc<MT, 64, 32>(a, grid, s);
+      else launch_bf16_dc<MT, 64, 64>(a, grid, s);
+    }
+  } else {
+    if (D == 128) launch_bf16_dc<MT, 128, 32>(a, grid, s);
+    else launch_bf16_dc<MT, 64, 32>(a, grid, s);
+  }
 }
 
 template <int MT>
@@ -619,8 +846,9 @@ int nsv_verify_attention(void* out, const void* q, const void* k_cache, const vo
   a.cu_seqlens_q = cu_seqlens_q;
   a.positions = positions;
   a.out = out;
-  a.part_o = need ? (float*)workspace : nullptr;
-  a.part_ml = need ? (float*)workspace + (size_t)B * Hkv * p.S * p.Mv * D : nullptr;
+  char* ws = (char*)workspace;
+  a.part_ml = need ? (float*)ws : nullptr;
+  a.part_o = need ? (float*)(ws + ml_bytes(B, Hkv, p)) : nullptr;
   a.scale_log2 = scale * 1.4426950408889634f;
   a.H = H;
   a.Hkv = Hkv;
@@ -631,9 +859,12 @@ int nsv_verify_attention(void* out, const void* q, const void* k_cache, const vo
   a.Mv = p.Mv;
   a.S = p.S;
   a.split_tokens = p.split;
+  a.npairs = B * Hkv;
+  a.P8 = (B * Hkv + 7) / 8;
+  a.dqc = p.dqc;
 
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid(p.S, Hkv, B);
+  const dim3 grid(8 * p.S * a.P8 * p.dqc);
   if (dtype == NSV_BF16) {
     switch (p.MT) {
       case 1: launch_bf16<1>(a, D, grid, s); break;
@@ -651,11 +882,12 @@ int nsv_verify_attention(void* out, const void* q, const void* k_cache, const vo
   }
   rc = nsv_launch_status();
   if (rc != NSV_OK || p.S <= 1) return rc;
-  const dim3 cgrid(p.Mv, Hkv, B);
+  const dim3 mgrid(p.Mv, B * Hkv);
+  const size_t msmem = (size_t)p.S * 2 * sizeof(float);
   if (dtype == NSV_BF16)
-    hipLaunchKernelGGL(verify_combine_kernel<bf16_t>, cgrid, dim3(128), 0, s, a, D);
+    hipLaunchKernelGGL(verify_merge_kernel<bf16_t>, mgrid, dim3(D), msmem, s, a, D);
   else
-    hipLaunchKernelGGL(verify_combine_kernel<float>, cgrid, dim3(128), 0, s, a, D);
+    hipLaunchKernelGGL(verify_merge_kernel<float>, mgrid, dim3(D), msmem, s, a, D);
   return nsv_launch_status();
 }
 

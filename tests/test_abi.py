@@ -51,14 +51,20 @@ def test_verify_attention_rejects_bad_shapes_before_launch():
     assert call(dt=7) == -1
     assert call(split=100) == -1     # split not a multiple of 128
     assert call(B=-1) == -1
-    assert call() == -3              # needs a workspace for 6 splits
+    assert call(split=128) == -3     # 12 key splits need a partials workspace
     assert call(B=0) == 0 and call(T=0) == 0
 
 
 def test_workspace_size_matches_split_plan():
     h = _lib.lib()
-    # config 2: 6 pages x 256 keys, auto split 128 -> 12 splits of 18 rows x (128 + 2) floats
-    assert h.nsv_verify_attention_workspace_size(8, 16, 8, 128, 256, 6, 9, 1, 0) == 8 * 8 * 12 * 18 * 130 * 4
+    # config 2 with 128-key splits: 6 pages x 256 keys -> 12 splits of 18 rows: (max, sum) pairs
+    # padded to 256 bytes, then 128-float partial rows
+    pad = lambda x: (x + 255) // 256 * 256
+    rows = 8 * 8 * 12 * 18
+    assert h.nsv_verify_attention_workspace_size(8, 16, 8, 128, 256, 6, 9, 1, 128) == pad(rows * 8) + rows * 512
+    # automatic plan for config 2: 64 (sequence, kv-head) pairs x 4 head-dim slices fill the
+    # chip, so every sequence is one split and no workspace is needed
+    assert h.nsv_verify_attention_workspace_size(8, 16, 8, 128, 256, 6, 9, 1, 0) == 0
     # one split: no workspace
     assert h.nsv_verify_attention_workspace_size(1, 16, 8, 128, 256, 1, 9, 1, 256) == 0
 
