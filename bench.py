@@ -143,6 +143,19 @@ def cpu_baseline(seconds: float) -> dict:
                       f"with {threads} threads"}
 
 
+def copy_probe(mib: int) -> None:
+    """Five plain device-to-device copies of ``mib`` MiB (reads and writes
+    exactly that many bytes each): the reference point for the HBM traffic
+    counters of the verify-attention kernel."""
+    n = mib << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_probe_bytes": n, "copies": 5}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -154,7 +167,13 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=2)
+    ap.add_argument("--copy-probe-mib", type=int, default=0,
+                    help="run only a plain device copy of this many MiB (calibrates rocprofv3's "
+                         "FETCH_SIZE / WRITE_SIZE counters against a known byte count) and exit")
     args = ap.parse_args()
+    if args.copy_probe_mib > 0:
+        copy_probe(args.copy_probe_mib)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus})",
               file=sys.stderr)

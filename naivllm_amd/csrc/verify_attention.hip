@@ -172,46 +172,62 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
   const int range_end = min(max_ctx, tok_begin + a.split_tokens);
   if (tok_begin >= max_ctx) return;
 
-  // ---- independent loads first: the split's block-table slice (into LDS),
-  // context length and query-row range; then Q and positions.
+  // ---- first round trip: the split's block-table slice, context length and
+  // query-row range, all independent
   const int pg0 = tok_begin >> a.bs_log2;
   const int npg = ((range_end - 1) >> a.bs_log2) - pg0 + 1;
-  {
-    const int32_t* btrow = a.block_tables + (int64_t)b * a.max_blocks + pg0;
-    for (int j = tid; j < npg; j += NT) pages[j] = btrow[j];
+  const int32_t* btrow = a.block_tables + (int64_t)b * a.max_blocks + pg0;
+  constexpr int PPT = (kMaxSplitPages + NT - 1) / NT;
+  int pv[PPT];
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) {
+    const int j = tid + i * NT;
+    pv[i] = j < npg ? btrow[j] : -1;
   }
   const int ctx = context_len(a, b);
   const int q0 = a.cu_seqlens_q[b];
   const int qlen = a.cu_seqlens_q[b + 1] - q0;
+  __builtin_amdgcn_sched_barrier(0);
   const int nsplit = splits_for(ctx, a.split_tokens);
-  if (split >= nsplit) return;  // uniform per workgroup
+  if (split >= nsplit || qlen < 0) return;  // uniform per workgroup
   const int tok_end = min(ctx, range_end);
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) {
+    const int j = tid + i * NT;
+    if (j < npg) pages[j] = pv[i];
+  }
 
-  // Q^T as the B operand: lane (g4, c) holds row m = 16*mt + c, dims 32*ks + 8*g4 .. +7.
-  // Rows outside the sequence read row 0 and keep position -1; rows at a
-  // negative position (outside the sequence or inert padding) are written
-  // as zeros, whatever they accumulated.
   bf16x8 qB[MT][KS];
   int qpos[MT];
-  int qmin = 0x7fffffff;  // lowest real query position of this lane's rows
+  int qmin = 0x7fffffff;
+  auto load_q = [&]() {
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    const int m = mt * 16 + c;
-    const int g = m / a.QL, t = m - g * a.QL;
-    const bool ok = (m < a.Mv) && (t < qlen);
-    const int row = ok ? q0 + t : 0;
-    const int gg = ok ? g : 0;
-    const int pos = (int)a.positions[row];
-    qpos[mt] = ok ? pos : -1;
-    if (qpos[mt] >= 0) qmin = min(qmin, qpos[mt]);
-    if (w == 0 && g4 == 0) row_pos[m] = qpos[mt];
-    const bf16_t* qrow = (const bf16_t*)a.q + ((int64_t)row * a.H + hk * a.G + gg) * DH;
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = mt * 16 + c;
+      const int g = m / a.QL, t = m - g * a.QL;
+      const bool ok = (m < a.Mv) && (t < qlen);
+      const int row = ok ? q0 + t : 0;
+      const int gg = ok ? g : 0;
+      qpos[mt] = (int)a.positions[row];
+      const bf16_t* qrow = (const bf16_t*)a.q + ((int64_t)row * a.H + hk * a.G + gg) * DH;
 #pragma unroll
-    for (int ks = 0; ks < KS; ++ks) qB[mt][ks] = as_bf16x8(load16(qrow + ks * 32 + g4 * 8));
-  }
+      for (int ks = 0; ks < KS; ++ks) qB[mt][ks] = as_bf16x8(load16(qrow + ks * 32 + g4 * 8));
+    }
+  };
+  auto finish_positions = [&]() {
 #pragma unroll
-  for (int o = 1; o < 16; o <<= 1) qmin = min(qmin, __shfl_xor(qmin, o, NSV_WAVE));
-  qmin = __builtin_amdgcn_readfirstlane(qmin);
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = mt * 16 + c;
+      const int g = m / a.QL, t = m - g * a.QL;
+      const bool ok = (m < a.Mv) && (t < qlen);
+      qpos[mt] = ok ? qpos[mt] : -1;
+      if (qpos[mt] >= 0) qmin = min(qmin, qpos[mt]);
+      if (w == 0 && g4 == 0) row_pos[m] = qpos[mt];
+    }
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) qmin = min(qmin, __shfl_xor(qmin, o, NSV_WAVE));
+    qmin = __builtin_amdgcn_readfirstlane(qmin);
+  };
 
   float m_run[MT], l_run[MT];  // running max of raw scores, running sum
   f32x4 acc[DT][MT];
@@ -400,14 +416,19 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
 
   // ---- two-stage pipeline over this wave's tiles
   Tile A, B;
+  load_q();
+  __builtin_amdgcn_sched_barrier(0);
   issue(A, 0);
+  issue(B, 1);
+  __builtin_amdgcn_sched_barrier(0);
+  finish_positions();
   for (int it = 0; it < niter; it += 2) {
-    issue(B, it + 1);
     __builtin_amdgcn_sched_barrier(0);
     compute(A);
     issue(A, it + 2);
     __builtin_amdgcn_sched_barrier(0);
     compute(B);
+    issue(B, it + 3);
   }
 
   // ---- merge the waves' (max, sum, O) ---------------------------------------

@@ -129,3 +129,30 @@ def test_store_kvcache_matches_oracle(dtype):
     torch.cuda.synchronize()
     assert np.array_equal(kc.float().cpu().numpy(), kc_ref)
     assert np.array_equal(vc.float().cpu().numpy(), vc_ref)
+
+
+@pytest.mark.parametrize("split", [128, 384])
+def test_repeated_calls_share_the_workspace(split):
+    # calls reuse one partials workspace: repeat the call (eagerly and under
+    # graph replay) and check each result
+    print(f"case: repeated split={split}", flush=True)
+    vb = synth.config2_batch()
+    want = _oracle(vb)
+    t = to_device(vb)
+    args = (t["query"], t["k_cache"], t["v_cache"], t["block_tables"], t["context_lens"], t["cu_seqlens_q"],
+            t["positions"], 1.0 / np.sqrt(128), 16, 8, 128, 256, 16)
+    for _ in range(3):
+        out = paged_attention_verify(*args, max_q_len=9, kv_split_tokens=split)
+        torch.cuda.synchronize()
+        assert_close(out, want, "bf16", f"eager split {split}")
+    out = torch.empty_like(t["query"])
+    paged_attention_verify(*args, max_q_len=9, kv_split_tokens=split, out=out)  # workspace allocated
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        paged_attention_verify(*args, max_q_len=9, kv_split_tokens=split, out=out)
+    for _ in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert_close(out, want, "bf16", f"graph split {split}")
