@@ -68,10 +68,66 @@ def attention_tiny():
     return case
 
 
+def _be_bytes(tokens):
+    return b"".join(int(t).to_bytes(4, "big") for t in tokens)
+
+
+def brute_ngram(history, k, min_n, max_n):
+    """The reference's lookup (drafters.py:63-83) by explicit byte scans:
+    right-most match of the suffix's big-endian bytes ending at or before
+    byte 4*(L-1); a hit inside a token restarts the scan left of it."""
+    L = len(history)
+    hay = _be_bytes(history)
+    for n in range(min(max_n, L - 1), min_n - 1, -1):
+        needle = hay[4 * (L - n):]
+        end = 4 * (L - 1)
+        while True:
+            idx = -1
+            for i in range(end - len(needle), -1, -1):
+                if hay[i:i + len(needle)] == needle:
+                    idx = i
+                    break
+            if idx == -1 or idx % 4 == 0:
+                break
+            end = idx
+        if idx != -1:
+            cont = history[idx // 4 + n: idx // 4 + n + k]
+            if cont:
+                return cont
+    return []
+
+
+def ngram_cases():
+    cases = []
+    fixed = [
+        ([16843009, 16843009, 16777216, 16777216, 16843009, 16843009], 3, 2, 3),  # straddling hit
+        ([256, 257, 16777216, 65793, 1, 65793, 257, 16777216], 3, 2, 3),
+        ([256, 512, 1, 2, 3, 256, 512], 2, 2, 2),
+        ([1, 2, 3, 1, 2], 8, 2, 8),
+        ([7, 7], 4, 1, 8),
+        ([7], 4, 1, 8),
+        ([], 4, 2, 8),
+        ([1, 2, 3, 4, 0, 2, 3, 9, 1, 2, 3], 1, 2, 3),
+    ]
+    for h, k, lo, hi in fixed:
+        cases.append(dict(history=h, k=k, min_n=lo, max_n=hi))
+    for seed in range(12):
+        vocab = [4, 50, 151936][seed % 3]
+        L = 20 + 7 * seed
+        h = [int(x) for x in synth.randint(seed, 40, L, 0, vocab)]
+        cases.append(dict(history=h, k=8, min_n=2, max_n=4 + seed % 5))
+    for c in cases:
+        c["expected"] = brute_ngram(c["history"], c["k"], c["min_n"], c["max_n"])
+    return cases
+
+
 def main():
     with open(os.path.join(HERE, "attention_tiny.json"), "w") as f:
         json.dump(attention_tiny(), f)
     print("wrote attention_tiny.json")
+    with open(os.path.join(HERE, "ngram_cases.json"), "w") as f:
+        json.dump(ngram_cases(), f)
+    print("wrote ngram_cases.json")
 
 
 if __name__ == "__main__":
