@@ -90,6 +90,64 @@ int nsv_store_kv(const void* key, const void* value, void* k_cache,
                  void* v_cache, const int64_t* slot_mapping, int T, int Hkv,
                  int D, int block_size, int dtype, void* stream);
 
+/*
+ * Acceptance (greedy exact-match, and min(1, p_t/p_d) rejection sampling
+ * with residual resampling), batched over B sequences with up to K drafts.
+ * Replaces src/myvllm/spec_engine/rejection_sampler.py:24-98
+ * (RejectionSampler.verify_greedy / verify_stochastic / verify) and the
+ * engine's batched argmax + per-sequence walk (spec_llm_engine.py:224-247).
+ *   target_logits  row r of sequence b at (b*target_seq_stride + r)*V,
+ *                  rows 0..num_drafts[b] (the verify forward's K+1 rows;
+ *                  graphed rounds pad each sequence to K+1 rows)
+ *   drafts [B, K] int32, num_drafts [B] int32 (clamped to 0..K)
+ *   out_tokens [B, K+1] int32: accepted drafts then the correction / bonus
+ *   token; out_len [B] int32 in 1..num_drafts[b]+1
+ * K <= 32.  Workspace: nsv_accept_workspace_size(B, K, V, dtype,
+ * stochastic); no initialisation needed.  Argmax ties go to the lowest
+ * index and NaN counts as the maximum, torch's rule.
+ */
+size_t nsv_accept_workspace_size(int B, int K, int V, int dtype, int stochastic);
+int nsv_accept_greedy(const void* target_logits, int64_t target_seq_stride,
+                      const int32_t* drafts, const int32_t* num_drafts, int B,
+                      int K, int V, int dtype, int32_t* out_tokens,
+                      int32_t* out_len, void* workspace,
+                      size_t workspace_bytes, void* stream);
+/*
+ * Stochastic acceptance.  temperature [B] fp32: a sequence with
+ * temperature <= 1e-6 is accepted greedily (rejection_sampler.py:95).
+ * draft_logits NULL: n-gram mode (:75-85): every row 0..num_drafts[b] is
+ * sampled and drafts are kept while they equal the samples; noise is
+ * [B, K+1, V].  Otherwise model mode (:51-73): draft row i of sequence b at
+ * (b*draft_seq_stride + i*draft_row_stride)*V; uniforms [B, K] fp32 decide
+ * u < min(1, p_t/p_d); one multinomial per sequence (the resample of the
+ * first rejected row, or the bonus) uses noise [B, V].  Randomness is input:
+ * torch.multinomial(p, 1) == argmax(p / q) for q = Exp(1) draws in p's dtype
+ * (noise has the logits dtype), so a caller drawing u = rand(K) and then q
+ * from the reference's generator reproduces its samples.
+ */
+int nsv_accept_stochastic(const void* target_logits, int64_t target_seq_stride,
+                          const void* draft_logits, int64_t draft_seq_stride,
+                          int64_t draft_row_stride, const int32_t* drafts,
+                          const int32_t* num_drafts, const float* temperature,
+                          const float* uniforms, const void* noise, int B,
+                          int K, int V, int dtype, int32_t* out_tokens,
+                          int32_t* out_len, void* workspace,
+                          size_t workspace_bytes, void* stream);
+
+/*
+ * N-gram (prompt-lookup) drafting on a device-resident token history.
+ * Replaces src/myvllm/spec_engine/drafters.py:63-83 (NgramDrafter._lookup,
+ * a bytes.rfind over the big-endian uint32 encoding of the history) and the
+ * token choice of NgramDrafter.draft (:46-61), byte-exact including matches
+ * at byte offsets inside a token.
+ *   history [B, hist_stride] int32, hist_len [B]: tokens of each sequence
+ *   out_drafts [B, K] int32, out_len [B] int32 (0: no match)
+ * 1 <= min_n <= max_n <= 64, 1 <= K <= 64.
+ */
+int nsv_ngram_draft(const int32_t* history, const int32_t* hist_len,
+                    int64_t hist_stride, int B, int min_n, int max_n, int K,
+                    int32_t* out_drafts, int32_t* out_len, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

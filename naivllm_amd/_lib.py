@@ -33,6 +33,13 @@ SIGNATURES: dict[str, tuple] = {
         _c_int,
         [_c_vp] * 8 + [_c_f32] + [_c_int] * 10 + [_c_vp, _c_size, _c_vp]),
     "nsv_store_kv": (_c_int, [_c_vp] * 5 + [_c_int] * 5 + [_c_vp]),
+    "nsv_accept_workspace_size": (_c_size, [_c_int] * 5),
+    "nsv_accept_greedy": (
+        _c_int, [_c_vp, _c_i64, _c_vp, _c_vp] + [_c_int] * 4 + [_c_vp, _c_vp, _c_vp, _c_size, _c_vp]),
+    "nsv_accept_stochastic": (
+        _c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_i64] + [_c_vp] * 5 + [_c_int] * 4
+        + [_c_vp, _c_vp, _c_vp, _c_size, _c_vp]),
+    "nsv_ngram_draft": (_c_int, [_c_vp, _c_vp, _c_i64] + [_c_int] * 4 + [_c_vp, _c_vp, _c_vp]),
 }
 
 _lib = None

@@ -82,3 +82,23 @@ def test_wrappers_raise_value_error_on_rejected_arguments():
         _lib.check(-2, "op")
     with pytest.raises(_lib.NaivspecError):
         _lib.check(1, "op")
+
+
+def test_accept_and_ngram_reject_bad_arguments_before_launch():
+    h = _lib.lib()
+    # K above 32, bad dtype, stride below K + 1, missing workspace
+    assert h.nsv_accept_greedy(1, 9, 1, 1, 2, 33, 100, 1, 1, 1, 1, 1 << 20, None) == -1
+    assert h.nsv_accept_greedy(1, 9, 1, 1, 2, 8, 100, 5, 1, 1, 1, 1 << 20, None) == -1
+    assert h.nsv_accept_greedy(1, 8, 1, 1, 2, 8, 100, 1, 1, 1, 1, 1 << 20, None) == -1
+    assert h.nsv_accept_greedy(1, 9, 1, 1, 2, 8, 100, 1, 1, 1, None, 0, None) == -3
+    assert h.nsv_accept_greedy(1, 9, 1, 1, 0, 8, 100, 1, 1, 1, None, 0, None) == 0   # empty batch
+    assert h.nsv_accept_workspace_size(2, 8, 100, 1, 0) > 0
+    assert h.nsv_accept_workspace_size(2, 8, 100, 1, 1) > h.nsv_accept_workspace_size(2, 8, 100, 1, 0)
+    # stochastic: model mode needs uniforms
+    assert h.nsv_accept_stochastic(1, 9, 1, 9, 1, 1, 1, 1, None, 1, 2, 8, 100, 1, 1, 1, 1, 1 << 30, None) == -1
+    # n-gram drafter: n range and continuation length
+    assert h.nsv_ngram_draft(1, 1, 10, 2, 0, 4, 8, 1, 1, None) == -1
+    assert h.nsv_ngram_draft(1, 1, 10, 2, 3, 2, 8, 1, 1, None) == -1
+    assert h.nsv_ngram_draft(1, 1, 10, 2, 2, 65, 8, 1, 1, None) == -1
+    assert h.nsv_ngram_draft(1, 1, 10, 2, 2, 4, 0, 1, 1, None) == -1
+    assert h.nsv_ngram_draft(1, 1, 10, 0, 2, 4, 8, 1, 1, None) == 0

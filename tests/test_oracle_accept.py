@@ -13,18 +13,19 @@ TDT = {"bf16": torch.bfloat16, "f32": torch.float32}
 
 def reference_torch(draft_tokens, target_rows, draft_rows, temperature, g):
     """The reference's sequence of torch calls (rejection_sampler.py:38-85),
-    executed by torch on the CPU with generator g — an independent
-    computation path (torch's softmax, multinomial and dtype promotion)."""
+    executed by torch on the device of its inputs with generator g — an
+    independent computation path (torch's softmax, multinomial and dtype
+    promotion)."""
     p_target = torch.softmax(target_rows / temperature, dim=-1)
     K = len(draft_tokens)
     acc = []
     if draft_rows is not None:
         p_draft = torch.softmax(draft_rows / temperature, dim=-1)
-        ids = torch.tensor(draft_tokens, dtype=torch.long)
+        ids = torch.tensor(draft_tokens, device=target_rows.device, dtype=torch.long)
         pd = p_draft.gather(1, ids[:, None]).squeeze(1)
         pt = p_target[:-1].gather(1, ids[:, None]).squeeze(1)
         ratio = (pt / pd.clamp_min(1e-20)).clamp(max=1.0)
-        u = torch.rand(K, generator=g)
+        u = torch.rand(K, device=target_rows.device, generator=g)
         for i in range(K):
             if u[i] < ratio[i]:
                 acc.append(draft_tokens[i])
