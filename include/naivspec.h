@@ -148,6 +148,42 @@ int nsv_ngram_draft(const int32_t* history, const int32_t* hist_len,
                     int64_t hist_stride, int B, int min_n, int max_n, int K,
                     int32_t* out_drafts, int32_t* out_len, void* stream);
 
+/*
+ * Verify-row metadata from the device-resident round state.
+ * Replaces the host row building of src/myvllm/engine/model_runner.py:
+ * 734-774 (_run_spec_verify_graph).  For each sequence b with active[b]
+ * and n = hist_len[b] > 0 tokens: rows b*(K+1) + j, j <= num_drafts[b],
+ * get token history[b, n-1] (j = 0) or drafts[b, j-1], position n-1+j and
+ * slot block_tables[b, pos / block_size] * block_size + pos % block_size;
+ * remaining rows are inert pads (id 0, position -1, slot -1) and
+ * context_lens[b] = n + num_drafts[b] (0 when inactive).  K + 1 <= 64.
+ */
+int nsv_prepare_verify(const int32_t* history, int64_t hist_stride,
+                       const int32_t* hist_len, const int32_t* drafts,
+                       const int32_t* num_drafts, const int32_t* block_tables,
+                       int max_blocks, int block_size, const int32_t* active,
+                       int B, int K, int64_t* input_ids, int64_t* positions,
+                       int64_t* slot_mapping, int64_t* context_lens,
+                       void* stream);
+
+/*
+ * Commit of accepted tokens into the device-resident history.
+ * Replaces src/myvllm/spec_engine/spec_llm_engine.py:249-291 (_commit):
+ * appends at most max_tokens[b] - (hist_len[b] - prompt_len[b]) of the
+ * num_tokens[b] accepted tokens, stopping after an eos token (unless
+ * ignore_eos[b]) or when the length reaches max_len[b] (> 0); clears
+ * active[b] when the sequence finishes (eos, max_tokens, max_len, or no
+ * room in the history for another round) and writes the count appended
+ * to committed[b].
+ */
+int nsv_commit(const int32_t* tokens, const int32_t* num_tokens,
+               const int32_t* num_drafts, int32_t* history,
+               int64_t hist_stride, int32_t* hist_len,
+               const int32_t* prompt_len, const int32_t* max_tokens,
+               const int32_t* max_len, const int32_t* ignore_eos, int eos,
+               int32_t* active, int32_t* committed, int B, int K,
+               void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -40,6 +40,10 @@ SIGNATURES: dict[str, tuple] = {
         _c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_i64] + [_c_vp] * 5 + [_c_int] * 4
         + [_c_vp, _c_vp, _c_vp, _c_size, _c_vp]),
     "nsv_ngram_draft": (_c_int, [_c_vp, _c_vp, _c_i64] + [_c_int] * 4 + [_c_vp, _c_vp, _c_vp]),
+    "nsv_prepare_verify": (
+        _c_int, [_c_vp, _c_i64] + [_c_vp] * 4 + [_c_int, _c_int, _c_vp, _c_int, _c_int] + [_c_vp] * 5),
+    "nsv_commit": (
+        _c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64] + [_c_vp] * 5 + [_c_int, _c_vp, _c_vp, _c_int, _c_int, _c_vp]),
 }
 
 _lib = None

@@ -1,0 +1,164 @@
+"""Qwen3 verify forward on the MI355X path.
+
+The target model of the verification round (src/myvllm/models/qwen3.py:
+Qwen3Attention :11-123, Qwen3MLP :129-151, Qwen3DecoderLayer :159-227,
+Qwen3Model :233-281, Qwen3ForCausalLM :287-344): embedding, N decoder
+layers (RMSNorm, fused QKV projection, per-head q/k RMSNorm, NeoX RoPE,
+paged KV store + paged verify attention, o_proj, RMSNorm with residual,
+SwiGLU MLP), final norm, LM head over every row.  The GEMMs, norms and RoPE
+are PyTorch-ROCm ops; the KV store and the attention are this library's
+gfx950 kernels.  Weights are random (seeded): no checkpoint is loaded.
+
+The forward takes the verify metadata explicitly (positions, slots, block
+tables, context lengths, cu_seqlens) so a whole forward is capturable in a
+hipGraph with static buffers, as the reference's verify graphs are
+(engine/model_runner.py:648-721).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+
+from naivllm_amd.layers.attention import paged_attention_verify, store_kvcache
+
+
+@dataclass
+class Qwen3Config:
+    vocab_size: int = 151936
+    hidden_size: int = 1024
+    num_layers: int = 28
+    num_heads: int = 16
+    num_kv_heads: int = 8
+    head_dim: int = 128
+    intermediate_size: int = 3072
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 1_000_000.0
+    max_position: int = 40960
+    tie_word_embeddings: bool = True
+
+    @staticmethod
+    def qwen3_0_6b(**kw) -> "Qwen3Config":
+        return Qwen3Config(**kw)
+
+    @staticmethod
+    def qwen3_8b(**kw) -> "Qwen3Config":
+        base = dict(hidden_size=4096, num_layers=36, num_heads=32, num_kv_heads=8, head_dim=128,
+                    intermediate_size=12288, tie_word_embeddings=False)
+        base.update(kw)
+        return Qwen3Config(**base)
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
+    """RMSNorm over the last dimension (layers/layernorm.py:18-25), with the
+    mean of squares taken in fp32."""
+    xf = x.float()
+    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(x.dtype) * weight
+
+
+def rope_cache(cfg: Qwen3Config, device) -> torch.Tensor:
+    """[max_position, head_dim] = [cos | sin] of NeoX rotary embedding
+    (layers/rotary_embedding.py:48-72)."""
+    d = cfg.head_dim
+    inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, d, 2, dtype=torch.float64) / d))
+    pos = torch.arange(cfg.max_position, dtype=torch.float64)
+    f = torch.outer(pos, inv)
+    return torch.cat([torch.cos(f), torch.sin(f)], dim=-1).float().to(device)
+
+
+def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Half-split rotation of [T, heads, D] (layers/rotary_embedding.py:4-23)."""
+    x1, x2 = x.chunk(2, dim=-1)
+    c, s = cos.unsqueeze(1), sin.unsqueeze(1)
+    return torch.cat([x1 * c - x2 * s, x1 * s + x2 * c], dim=-1)
+
+
+class Qwen3Verify:
+    """Random-init Qwen3 weights plus the verify forward."""
+
+    def __init__(self, cfg: Qwen3Config, device, dtype=torch.bfloat16, seed: int = 0, std: float = 0.02):
+        self.cfg = cfg
+        self.device = torch.device(device)
+        self.dtype = dtype
+        g = torch.Generator(device=self.device)
+        g.manual_seed(seed)
+
+        def w(*shape, scale=std):
+            return (torch.randn(*shape, generator=g, device=self.device, dtype=torch.float32) * scale).to(dtype)
+
+        H, Hkv, D, E = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.hidden_size
+        self.embed = w(cfg.vocab_size, E, scale=1.0)
+        self.layers = []
+        for _ in range(cfg.num_layers):
+            self.layers.append(dict(
+                ln1=torch.ones(E, device=self.device, dtype=dtype),
+                qkv=w((H + 2 * Hkv) * D, E, scale=1.0 / math.sqrt(E)),
+                q_norm=torch.ones(D, device=self.device, dtype=dtype),
+                k_norm=torch.ones(D, device=self.device, dtype=dtype),
+                o=w(E, H * D, scale=1.0 / math.sqrt(H * D)),
+                ln2=torch.ones(E, device=self.device, dtype=dtype),
+                gate_up=w(2 * cfg.intermediate_size, E, scale=1.0 / math.sqrt(E)),
+                down=w(E, cfg.intermediate_size, scale=1.0 / math.sqrt(cfg.intermediate_size)),
+            ))
+        self.norm = torch.ones(E, device=self.device, dtype=dtype)
+        self.lm_head = self.embed if cfg.tie_word_embeddings else w(cfg.vocab_size, E, scale=1.0 / math.sqrt(E))
+        self.rope = rope_cache(cfg, self.device)
+        self.scale = 1.0 / math.sqrt(D)
+        self.k_caches: list[torch.Tensor] = []
+        self.v_caches: list[torch.Tensor] = []
+        self.block_size = 0
+
+    def allocate_kv_cache(self, num_blocks: int, block_size: int) -> None:
+        """One [num_blocks, block_size, Hkv, D] K and V pool per layer
+        (engine/model_runner.py:244-279 keeps one [2, L, ...] tensor)."""
+        cfg = self.cfg
+        shape = (num_blocks, block_size, cfg.num_kv_heads, cfg.head_dim)
+        self.k_caches = [torch.zeros(shape, device=self.device, dtype=self.dtype) for _ in range(cfg.num_layers)]
+        self.v_caches = [torch.zeros(shape, device=self.device, dtype=self.dtype) for _ in range(cfg.num_layers)]
+        self.block_size = block_size
+
+    def forward(self, input_ids: torch.Tensor, positions: torch.Tensor, slot_mapping: torch.Tensor,
+                block_tables: torch.Tensor, context_lens: torch.Tensor, cu_seqlens_q: torch.Tensor,
+                max_q_len: int, logits_out: torch.Tensor | None = None) -> torch.Tensor:
+        """Verify forward over T = sum of per-sequence query rows.  Rows at
+        position -1 are inert padding (no KV store, zero attention output).
+        Returns logits [T, vocab] (written into logits_out when given)."""
+        cfg = self.cfg
+        H, Hkv, D = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim
+        T = input_ids.shape[0]
+        cs = self.rope[positions.clamp(min=0)]
+        cos, sin = cs[:, :D // 2].to(self.dtype), cs[:, D // 2:].to(self.dtype)
+        x = F.embedding(input_ids, self.embed)
+        residual = None
+        for li, L in enumerate(self.layers):
+            if residual is None:
+                residual = x
+                h = rms_norm(x, L["ln1"], cfg.rms_norm_eps)
+            else:
+                residual = x + residual
+                h = rms_norm(residual, L["ln1"], cfg.rms_norm_eps)
+            qkv = F.linear(h, L["qkv"])
+            q, k, v = qkv.split([H * D, Hkv * D, Hkv * D], dim=-1)
+            q = rms_norm(q.view(T, H, D), L["q_norm"], cfg.rms_norm_eps)
+            k = rms_norm(k.view(T, Hkv, D), L["k_norm"], cfg.rms_norm_eps)
+            q = apply_rope(q, cos, sin)
+            k = apply_rope(k, cos, sin)
+            v = v.reshape(T, Hkv, D)
+            store_kvcache(k, v, self.k_caches[li], self.v_caches[li], slot_mapping, self.block_size)
+            o = paged_attention_verify(q, self.k_caches[li], self.v_caches[li], block_tables, context_lens,
+                                       cu_seqlens_q, positions, self.scale, H, Hkv, D, self.block_size,
+                                       max(16, 1 << (max_q_len - 1).bit_length()), max_q_len=max_q_len)
+            x = F.linear(o.view(T, H * D), L["o"])
+            residual = x + residual
+            h = rms_norm(residual, L["ln2"], cfg.rms_norm_eps)
+            gu = F.linear(h, L["gate_up"])
+            g_, u_ = gu.chunk(2, dim=-1)
+            x = F.linear(F.silu(g_) * u_, L["down"])
+        h = rms_norm(x + residual, self.norm, cfg.rms_norm_eps)
+        if logits_out is None:
+            return F.linear(h, self.lm_head)
+        torch.matmul(h, self.lm_head.t(), out=logits_out)
+        return logits_out
