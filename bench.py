@@ -104,6 +104,59 @@ class Workload:
             self.call(layer, split)
 
 
+def config3_prompts(batch: int, seed: int = 3, prefix: int = 1200, span: int = 40, vocab: int = 151936):
+    """BASELINE config 3 prompts: a 1200-token document made of 40-token
+    spans that recur across it (span i at chapter positions i and 7i mod N,
+    after benchmarks/rag_bench.py:80-105), followed per request by the
+    first tokens of one span as the question, so an answer quoting the
+    document is n-gram draftable."""
+    nspans = 12
+    spans = [[int(x) for x in synth.randint(seed, 90 + i, span, 100, vocab)] for i in range(nspans)]
+    doc = []
+    i = 0
+    while len(doc) < prefix:
+        doc += spans[i % nspans] + spans[(i * 7) % nspans][: span // 4]
+        i += 1
+    doc = doc[:prefix]
+    return [doc + spans[(b * 5 + 1) % nspans][:6] for b in range(batch)]
+
+
+def e2e_round(batches=(1, 8), tokens: int = 48, K: int = 8) -> dict:
+    """the whole greedy n-gram verification round of a
+    random-init Qwen3-0.6B (28 layers, bf16), one hipGraph replay per round
+    per batch bucket; decode tokens per second over the rounds (prefill
+    excluded, reported apart)."""
+    from naivllm_amd.sampling_parameters import SamplingParams
+    from naivllm_amd.spec_engine.spec_llm_engine import SpecLLMEngine
+
+    eng = SpecLLMEngine(dict(spec_method="ngram", num_speculative_tokens=K, ngram_min_size=2, ngram_max_size=4,
+                             max_num_sequences=max(batches), max_model_length=1200 + 16 + tokens + 64,
+                             block_size=256, seed=0))
+    sp = SamplingParams(temperature=0.0, max_tokens=tokens, ignore_eos=True)
+    out = {}
+    for b in batches:
+        before = dict(eng.spec_stats)
+        res = eng.generate(config3_prompts(b), sp)
+        m = res["metrics"]
+        st = m["spec_decoding"]
+        drafted = st["drafted_tokens"] - before["drafted_tokens"]
+        accepted = st["accepted_tokens"] - before["accepted_tokens"]
+        out[f"b{b}"] = {
+            "decode_tok_s": round(m["decode_tok_per_s"], 1),
+            "decode_ms_per_round": round(1e3 * m["decode_s"] / max(m["rounds"], 1), 3),
+            "rounds": m["rounds"],
+            "tokens_per_round": round(m["decode_tokens"] / max(m["rounds"], 1), 3),
+            "drafted": drafted,
+            "accepted": accepted,
+            "prefill_s": round(m["prefill_s"], 3),
+            "output_tokens": m["output_tokens"],
+        }
+        print(f"[bench] e2e b{b}: {out[f'b{b}']}", file=sys.stderr, flush=True)
+    del eng
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(seconds: float) -> dict:
     """The torch-on-CPU restatement of the same verify-attention call
     (config 2 shape, one layer), timed on this host's cores."""
@@ -166,6 +219,7 @@ def main():
     ap.add_argument("--split", type=int, default=0, help="keys per workgroup split (0 = automatic)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the config-3 end-to-end round measurement")
     ap.add_argument("--seed", type=int, default=2)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run only a plain device copy of this many MiB (calibrates rocprofv3's "
@@ -213,6 +267,7 @@ def main():
     print(f"[bench] {calls} calls, {us_per_call:.2f} us/call, {gbs:.1f} GB/s, {tflops:.1f} TFLOP/s",
           file=sys.stderr, flush=True)
 
+    e2e = None if args.no_e2e else e2e_round()
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     line = {
         "metric": METRIC,
@@ -236,6 +291,7 @@ def main():
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "bytes_per_call": wl.bytes, "mfma_tflops": round(tflops, 2),
                      "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 5)},
+        "accepted_tok_s": e2e,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
