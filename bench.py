@@ -104,6 +104,21 @@ class Workload:
             self.call(layer, split)
 
 
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "verify_attn_config2_traffic.md")
+
+
+def measured_traffic(workload_config: int):
+    """HBM bytes per verify-attention launch from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes (copy-calibrated), for the config-2
+    workload those passes ran; None otherwise."""
+    if workload_config != 2 or not os.path.exists(TRAFFIC_PROFILE):
+        return None
+    for line in open(TRAFFIC_PROFILE):
+        if line.startswith("traffic_bytes:"):
+            return int(line.split(":")[1])
+    return None
+
+
 def config3_prompts(batch: int, seed: int = 3, prefix: int = 1200, span: int = 40, vocab: int = 151936):
     """BASELINE config 3 prompts: a 1200-token document made of 40-token
     spans that recur across it (span i at chapter positions i and 7i mod N,
@@ -288,7 +303,8 @@ def main():
         "pct_of_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
         "us_per_call": round(us_per_call, 3),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.config),
+                     "traffic_source": "profiles/verify_attn_config2_traffic.md (rocprofv3 FETCH_SIZE x2 + WRITE_SIZE x1)",
                      "bytes_per_call": wl.bytes, "mfma_tflops": round(tflops, 2),
                      "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 5)},
         "accepted_tok_s": e2e,
