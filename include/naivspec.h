@@ -184,6 +184,33 @@ int nsv_commit(const int32_t* tokens, const int32_t* num_tokens,
                int32_t* active, int32_t* committed, int B, int K,
                void* stream);
 
+/*
+ * Fused elementwise stages of the Qwen3 verify forward (bf16 only).
+ * nsv_rms_norm: out = rmsnorm(r) * weight with r = x + residual (or x when
+ *   residual is NULL), r written to residual_out when not NULL; rows of E
+ *   <= 4096.  Replaces layers/layernorm.py:18-35 (LayerNorm.forward with
+ *   and without residual).
+ * nsv_qk_norm_rope_store: the pre-attention epilogue over qkv
+ *   [T, (H + 2*Hkv) * D]: per-head RMSNorm of q and k (q_norm_w, k_norm_w
+ *   [D]), NeoX rotation at positions[t] from cos_sin [max_pos, D] (fp32,
+ *   cos then sin), q written to q_out [T, H, D], k and v stored into the
+ *   paged caches at slot_mapping[t] (slot < 0: not stored).  D even,
+ *   <= 128.  Replaces models/qwen3.py:100-119 + layers/rotary_embedding.py:
+ *   78-86 + layers/attention.py:71-112.
+ * nsv_silu_mul: out [T, I] = silu(gate_up[:, :I]) * gate_up[:, I:].
+ *   Replaces layers/activation.py:17-19.
+ */
+int nsv_rms_norm(const void* x, const void* residual, void* residual_out,
+                 const void* weight, void* out, int T, int E, float eps,
+                 void* stream);
+int nsv_qk_norm_rope_store(const void* qkv, const void* q_norm_w,
+                           const void* k_norm_w, const float* cos_sin,
+                           int max_pos, const int64_t* positions,
+                           const int64_t* slot_mapping, void* q_out,
+                           void* k_cache, void* v_cache, int T, int H,
+                           int Hkv, int D, float eps, void* stream);
+int nsv_silu_mul(const void* gate_up, void* out, int T, int I, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

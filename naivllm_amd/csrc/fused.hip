@@ -1,0 +1,183 @@
+// Fused elementwise stages of the Qwen3 verify forward for gfx950 (bf16).
+//
+// The reference composes these from separate torch ops (each a kernel
+// launch and an HBM round trip of the activations):
+//   * residual add + RMSNorm: layers/layernorm.py:18-35;
+//   * per-head q/k RMSNorm, NeoX rotary embedding and the paged KV store:
+//     models/qwen3.py:100-119, layers/rotary_embedding.py:4-86 and
+//     layers/attention.py:9-112 (store_kvcache) -- the pre-attention
+//     epilogue, one kernel here;
+//   * SiLU(gate) * up: layers/activation.py:17-19.
+// Arithmetic is fp32 inside each kernel with one bf16 rounding per output.
+
+#include "common.h"
+
+namespace {
+
+__device__ __forceinline__ float bf(uint16_t b) { return bf16_bits_to_f32(b); }
+
+// ---------------------------------------------------------------------------
+// out = rmsnorm(r) * w, r = x + residual (residual may be null: r = x);
+// r is written to residual_out when given.  One workgroup per row.
+// ---------------------------------------------------------------------------
+constexpr int kNormThreads = 256;
+
+__global__ __launch_bounds__(kNormThreads) void rms_norm_residual_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ residual, uint16_t* __restrict__ residual_out,
+    const uint16_t* __restrict__ w, uint16_t* __restrict__ out, int E, float eps) {
+  __shared__ float red[kNormThreads / 64];
+  const int64_t row = blockIdx.x;
+  const uint16_t* xr = x + row * E;
+  const uint16_t* rr = residual ? residual + row * E : nullptr;
+  float ss = 0.f;
+  // thread t handles elements t, t + 256, ... (E <= 16 * 256), kept in registers
+  float v[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int i = threadIdx.x + j * kNormThreads;
+    v[j] = 0.f;
+    if (i < E) {
+      float r = bf(xr[i]);
+      if (rr) r = bf16_bits_to_f32(f32_to_bf16_bits(r + bf(rr[i])));  // the residual stream is bf16
+      v[j] = r;
+      ss += r * r;
+    }
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormThreads / 64; ++i) tot += red[i];
+  const float inv = rsqrtf(tot / (float)E + eps);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int i = threadIdx.x + j * kNormThreads;
+    if (i < E) {
+      if (residual_out) residual_out[row * E + i] = f32_to_bf16_bits(v[j]);
+      out[row * E + i] = f32_to_bf16_bits(v[j] * inv * bf(w[i]));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Pre-attention epilogue.  qkv [T, (H + 2*Hkv) * D]: one wave per (row,
+// head); lane l holds elements l and l + D/2 (exactly the NeoX rotation
+// pair), D/2 <= 64.  q heads: RMSNorm * q_w, rotate, write q_out [T, H, D].
+// k heads: RMSNorm * k_w, rotate, store at the row's slot.  v heads: store.
+// Rows with slot < 0 store nothing; rows with position < 0 use position 0.
+// ---------------------------------------------------------------------------
+struct EpilogueArgs {
+  const uint16_t* qkv;
+  const uint16_t* q_w;
+  const uint16_t* k_w;
+  const float* cos_sin;  // [max_pos, D]: cos in [0, D/2), sin in [D/2, D)
+  const int64_t* positions;
+  const int64_t* slots;
+  uint16_t* q_out;
+  uint16_t* k_cache;  // [num_blocks * block_size, Hkv, D]
+  uint16_t* v_cache;
+  int T, H, Hkv, D, max_pos;
+  float eps;
+};
+
+__global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(EpilogueArgs a) {
+  const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
+  const int lane = threadIdx.x & 63;
+  const int heads = a.H + 2 * a.Hkv;
+  if (wave >= a.T * heads) return;
+  const int row = wave / heads, head = wave - row * heads;
+  const int half = a.D >> 1;
+  const bool on = lane < half;
+  const uint16_t* src = a.qkv + ((int64_t)row * heads + head) * a.D;
+  float x1 = on ? bf(src[lane]) : 0.f;
+  float x2 = on ? bf(src[lane + half]) : 0.f;
+  const int64_t slot = a.slots[row];
+  if (head >= a.H + a.Hkv) {  // v head: store as is
+    if (on && slot >= 0) {
+      uint16_t* dst = a.v_cache + (slot * a.Hkv + (head - a.H - a.Hkv)) * a.D;
+      dst[lane] = src[lane];
+      dst[lane + half] = src[lane + half];
+    }
+    return;
+  }
+  const bool is_q = head < a.H;
+  const float ms = wave_sum(x1 * x1 + x2 * x2) / (float)a.D;
+  const float inv = rsqrtf(ms + a.eps);
+  const uint16_t* w = is_q ? a.q_w : a.k_w;
+  if (on) {
+    // the normalised value is bf16 in the reference (q_norm/k_norm output)
+    x1 = bf16_bits_to_f32(f32_to_bf16_bits(x1 * inv * bf(w[lane])));
+    x2 = bf16_bits_to_f32(f32_to_bf16_bits(x2 * inv * bf(w[lane + half])));
+    int64_t pos = a.positions[row];
+    pos = pos < 0 ? 0 : (pos >= a.max_pos ? a.max_pos - 1 : pos);
+    const float c = a.cos_sin[pos * a.D + lane], s = a.cos_sin[pos * a.D + half + lane];
+    const uint16_t o1 = f32_to_bf16_bits(x1 * c - x2 * s);
+    const uint16_t o2 = f32_to_bf16_bits(x1 * s + x2 * c);
+    if (is_q) {
+      uint16_t* dst = a.q_out + ((int64_t)row * a.H + head) * a.D;
+      dst[lane] = o1;
+      dst[lane + half] = o2;
+    } else if (slot >= 0) {
+      uint16_t* dst = a.k_cache + (slot * a.Hkv + (head - a.H)) * a.D;
+      dst[lane] = o1;
+      dst[lane + half] = o2;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// out[t, i] = silu(gu[t, i]) * gu[t, I + i]
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t* __restrict__ gu, uint16_t* __restrict__ out,
+                                                       int64_t T, int I) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= T * I) return;
+  const int64_t t = idx / I;
+  const int i = (int)(idx - t * I);
+  const float g = bf(gu[t * 2 * I + i]);
+  const float u = bf(gu[t * 2 * I + I + i]);
+  out[idx] = f32_to_bf16_bits(g / (1.f + __expf(-g)) * u);
+}
+
+}  // namespace
+
+extern "C" {
+
+int nsv_rms_norm(const void* x, const void* residual, void* residual_out, const void* weight, void* out, int T,
+                 int E, float eps, void* stream) {
+  if (T < 0 || E <= 0 || E > 16 * kNormThreads) return NSV_ERR_ARG;
+  if (T == 0) return NSV_OK;
+  if (!x || !weight || !out) return NSV_ERR_ARG;
+  hipLaunchKernelGGL(rms_norm_residual_kernel, dim3(T), dim3(kNormThreads), 0, (hipStream_t)stream,
+                     (const uint16_t*)x, (const uint16_t*)residual, (uint16_t*)residual_out, (const uint16_t*)weight,
+                     (uint16_t*)out, E, eps);
+  return nsv_launch_status();
+}
+
+int nsv_qk_norm_rope_store(const void* qkv, const void* q_norm_w, const void* k_norm_w, const float* cos_sin,
+                           int max_pos, const int64_t* positions, const int64_t* slot_mapping, void* q_out,
+                           void* k_cache, void* v_cache, int T, int H, int Hkv, int D, float eps, void* stream) {
+  if (T < 0 || H <= 0 || Hkv <= 0 || D <= 0 || (D & 1) || D > 128 || max_pos <= 0) return NSV_ERR_ARG;
+  if (T == 0) return NSV_OK;
+  if (!qkv || !q_norm_w || !k_norm_w || !cos_sin || !positions || !slot_mapping || !q_out || !k_cache || !v_cache)
+    return NSV_ERR_ARG;
+  EpilogueArgs a{(const uint16_t*)qkv, (const uint16_t*)q_norm_w, (const uint16_t*)k_norm_w, cos_sin, positions,
+                 slot_mapping, (uint16_t*)q_out, (uint16_t*)k_cache, (uint16_t*)v_cache, T, H, Hkv, D, max_pos, eps};
+  const int64_t waves = (int64_t)T * (H + 2 * Hkv);
+  hipLaunchKernelGGL(qk_norm_rope_store_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, (hipStream_t)stream,
+                     a);
+  return nsv_launch_status();
+}
+
+int nsv_silu_mul(const void* gate_up, void* out, int T, int I, void* stream) {
+  if (T < 0 || I <= 0) return NSV_ERR_ARG;
+  if (T == 0) return NSV_OK;
+  if (!gate_up || !out) return NSV_ERR_ARG;
+  const int64_t n = (int64_t)T * I;
+  hipLaunchKernelGGL(silu_mul_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)gate_up, (uint16_t*)out, (int64_t)T, I);
+  return nsv_launch_status();
+}
+
+}  // extern "C"

@@ -5,9 +5,12 @@ Qwen3Attention :11-123, Qwen3MLP :129-151, Qwen3DecoderLayer :159-227,
 Qwen3Model :233-281, Qwen3ForCausalLM :287-344): embedding, N decoder
 layers (RMSNorm, fused QKV projection, per-head q/k RMSNorm, NeoX RoPE,
 paged KV store + paged verify attention, o_proj, RMSNorm with residual,
-SwiGLU MLP), final norm, LM head over every row.  The GEMMs, norms and RoPE
-are PyTorch-ROCm ops; the KV store and the attention are this library's
-gfx950 kernels.  Weights are random (seeded): no checkpoint is loaded.
+SwiGLU MLP), final norm, LM head over every row.  The four GEMMs per layer
+and the LM head are PyTorch-ROCm (hipBLASLt); everything between them is
+this library's gfx950 kernels: residual add + RMSNorm, the pre-attention
+epilogue (q/k RMSNorm + RoPE + paged KV store), verify attention and
+SiLU * up -- 4 GEMMs + 4 kernels per layer.  Weights are random (seeded):
+no checkpoint is loaded.
 
 The forward takes the verify metadata explicitly (positions, slots, block
 tables, context lengths, cu_seqlens) so a whole forward is capturable in a
@@ -23,7 +26,8 @@ from dataclasses import dataclass
 import torch
 import torch.nn.functional as F
 
-from naivllm_amd.layers.attention import paged_attention_verify, store_kvcache
+from naivllm_amd import _lib
+from naivllm_amd.layers.attention import paged_attention_verify
 
 
 @dataclass
@@ -52,28 +56,39 @@ class Qwen3Config:
         return Qwen3Config(**base)
 
 
-def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float) -> torch.Tensor:
-    """RMSNorm over the last dimension (layers/layernorm.py:18-25), with the
-    mean of squares taken in fp32."""
-    xf = x.float()
-    return (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)).to(x.dtype) * weight
-
-
 def rope_cache(cfg: Qwen3Config, device) -> torch.Tensor:
     """[max_position, head_dim] = [cos | sin] of NeoX rotary embedding
-    (layers/rotary_embedding.py:48-72)."""
+    (layers/rotary_embedding.py:48-72), fp32."""
     d = cfg.head_dim
     inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, d, 2, dtype=torch.float64) / d))
     pos = torch.arange(cfg.max_position, dtype=torch.float64)
     f = torch.outer(pos, inv)
-    return torch.cat([torch.cos(f), torch.sin(f)], dim=-1).float().to(device)
+    return torch.cat([torch.cos(f), torch.sin(f)], dim=-1).float().contiguous().to(device)
 
 
-def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
-    """Half-split rotation of [T, heads, D] (layers/rotary_embedding.py:4-23)."""
-    x1, x2 = x.chunk(2, dim=-1)
-    c, s = cos.unsqueeze(1), sin.unsqueeze(1)
-    return torch.cat([x1 * c - x2 * s, x1 * s + x2 * c], dim=-1)
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, out: torch.Tensor,
+             residual: torch.Tensor | None = None, residual_out: torch.Tensor | None = None) -> None:
+    """out = rmsnorm(x + residual) * weight; x + residual goes to
+    residual_out (layers/layernorm.py:18-35)."""
+    T, E = x.shape
+    rc = _lib.lib().nsv_rms_norm(x.data_ptr(), _lib.ptr(residual), _lib.ptr(residual_out), weight.data_ptr(),
+                                 out.data_ptr(), T, E, eps, _lib.stream_ptr(x.device))
+    _lib.check(rc, "rms_norm")
+
+
+def qk_norm_rope_store(qkv, q_norm_w, k_norm_w, cos_sin, positions, slot_mapping, q_out, k_cache, v_cache,
+                       H: int, Hkv: int, D: int, eps: float) -> None:
+    rc = _lib.lib().nsv_qk_norm_rope_store(
+        qkv.data_ptr(), q_norm_w.data_ptr(), k_norm_w.data_ptr(), cos_sin.data_ptr(), cos_sin.shape[0],
+        positions.data_ptr(), slot_mapping.data_ptr(), q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+        qkv.shape[0], H, Hkv, D, eps, _lib.stream_ptr(qkv.device))
+    _lib.check(rc, "qk_norm_rope_store")
+
+
+def silu_mul(gate_up: torch.Tensor, out: torch.Tensor) -> None:
+    rc = _lib.lib().nsv_silu_mul(gate_up.data_ptr(), out.data_ptr(), gate_up.shape[0], out.shape[1],
+                                 _lib.stream_ptr(gate_up.device))
+    _lib.check(rc, "silu_mul")
 
 
 class Qwen3Verify:
@@ -126,38 +141,34 @@ class Qwen3Verify:
         """Verify forward over T = sum of per-sequence query rows.  Rows at
         position -1 are inert padding (no KV store, zero attention output).
         Returns logits [T, vocab] (written into logits_out when given)."""
+        if self.dtype != torch.bfloat16:
+            raise ValueError("the fused forward kernels are bf16")
         cfg = self.cfg
-        H, Hkv, D = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim
+        H, Hkv, D, E = cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, cfg.hidden_size
+        eps = cfg.rms_norm_eps
         T = input_ids.shape[0]
-        cs = self.rope[positions.clamp(min=0)]
-        cos, sin = cs[:, :D // 2].to(self.dtype), cs[:, D // 2:].to(self.dtype)
+        block_m = max(16, 1 << (max_q_len - 1).bit_length())
         x = F.embedding(input_ids, self.embed)
-        residual = None
+        residual = torch.empty_like(x)
+        h = torch.empty_like(x)
+        q = torch.empty(T, H, D, dtype=self.dtype, device=self.device)
+        act = torch.empty(T, cfg.intermediate_size, dtype=self.dtype, device=self.device)
         for li, L in enumerate(self.layers):
-            if residual is None:
-                residual = x
-                h = rms_norm(x, L["ln1"], cfg.rms_norm_eps)
+            if li == 0:
+                rms_norm(x, L["ln1"], eps, h, residual_out=residual)
             else:
-                residual = x + residual
-                h = rms_norm(residual, L["ln1"], cfg.rms_norm_eps)
+                rms_norm(x, L["ln1"], eps, h, residual=residual, residual_out=residual)
             qkv = F.linear(h, L["qkv"])
-            q, k, v = qkv.split([H * D, Hkv * D, Hkv * D], dim=-1)
-            q = rms_norm(q.view(T, H, D), L["q_norm"], cfg.rms_norm_eps)
-            k = rms_norm(k.view(T, Hkv, D), L["k_norm"], cfg.rms_norm_eps)
-            q = apply_rope(q, cos, sin)
-            k = apply_rope(k, cos, sin)
-            v = v.reshape(T, Hkv, D)
-            store_kvcache(k, v, self.k_caches[li], self.v_caches[li], slot_mapping, self.block_size)
+            qk_norm_rope_store(qkv, L["q_norm"], L["k_norm"], self.rope, positions, slot_mapping, q,
+                               self.k_caches[li], self.v_caches[li], H, Hkv, D, eps)
             o = paged_attention_verify(q, self.k_caches[li], self.v_caches[li], block_tables, context_lens,
-                                       cu_seqlens_q, positions, self.scale, H, Hkv, D, self.block_size,
-                                       max(16, 1 << (max_q_len - 1).bit_length()), max_q_len=max_q_len)
+                                       cu_seqlens_q, positions, self.scale, H, Hkv, D, self.block_size, block_m,
+                                       max_q_len=max_q_len)
             x = F.linear(o.view(T, H * D), L["o"])
-            residual = x + residual
-            h = rms_norm(residual, L["ln2"], cfg.rms_norm_eps)
-            gu = F.linear(h, L["gate_up"])
-            g_, u_ = gu.chunk(2, dim=-1)
-            x = F.linear(F.silu(g_) * u_, L["down"])
-        h = rms_norm(x + residual, self.norm, cfg.rms_norm_eps)
+            rms_norm(x, L["ln2"], eps, h, residual=residual, residual_out=residual)
+            silu_mul(F.linear(h, L["gate_up"]), act)
+            x = F.linear(act, L["down"])
+        rms_norm(x, self.norm, eps, h, residual=residual)
         if logits_out is None:
             return F.linear(h, self.lm_head)
         torch.matmul(h, self.lm_head.t(), out=logits_out)
