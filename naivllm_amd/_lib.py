@@ -102,19 +102,27 @@ def ptr(t: torch.Tensor | None) -> int | None:
 
 
 _workspaces: dict = {}
+_retired: list = []
 
 
-def workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
-    """Per-device scratch buffer for the kernels' split partials, grown on
-    demand and reused by every call on the device (so calls must be ordered
-    on one stream, as torch's current stream orders them)."""
+def workspace(device: torch.device, nbytes: int, name: str) -> torch.Tensor | None:
+    """Per-(device, operator) scratch buffer, grown on demand and reused by
+    every call of that operator on the device (so calls must be ordered on
+    one stream, as torch's current stream orders them).
+
+    Buffers start zero-filled: verify attention keeps per-pair arrival
+    counters at the front of its workspace, which every call leaves at zero.
+    A buffer replaced by a larger one is kept alive, so a graph captured
+    with the old one never points at freed memory."""
     if nbytes <= 0:
         return None
-    key = (device.type, device.index if device.index is not None else torch.cuda.current_device())
+    key = (device.type, device.index if device.index is not None else torch.cuda.current_device(), name)
     buf = _workspaces.get(key)
     if buf is None or buf.numel() < nbytes:
         size = max(nbytes, 2 * (buf.numel() if buf is not None else 0))
         size = (size + 255) // 256 * 256
-        buf = torch.empty(size, dtype=torch.uint8, device=device)
+        if buf is not None:
+            _retired.append(buf)
+        buf = torch.zeros(size, dtype=torch.uint8, device=device)
         _workspaces[key] = buf
     return buf

@@ -2,39 +2,55 @@
 //
 // Behaviour follows the reference's Triton path
 // (src/myvllm/layers/attention.py:522-668 verify, :9-112 KV store); the
-// decomposition is this library's own:
+// decomposition is this library's own.  Common to the bf16 kernels:
 //
-//   * one workgroup per (sequence, kv-head, key split).  The workgroup reads
-//     each K/V byte of its split exactly once and serves every query row of
-//     the GQA group from it (the reference re-reads K/V once per query head);
-//   * the query rows of a GQA group are packed into the M dimension of a
-//     16x16x32 bf16 MFMA: rows m = g * QL + t for group member g and
-//     verify row t, padded to 16 * MT rows;
+//   * a workgroup serves one (sequence, kv-head) pair -- every query row of
+//     its GQA group -- from one read of the pair's K/V (the reference
+//     re-reads K/V once per query head);
+//   * the group's query rows are packed into 16-row MFMA tiles: rows
+//     m = g * QL + t for group member g and verify row t;
 //   * S^T = K Q^T is computed so that the MFMA result layout is directly the
 //     B operand of O^T = V^T P^T (no register shuffles between the two
-//     products); V is staged through LDS once per 32-key tile and read back
-//     transposed;
-//   * a tile's page ids are read once (one lane per key) and broadcast with
-//     lane shuffles, the next tile's ids are prefetched, and every K/V load
-//     is unconditional (masked keys read a valid dummy row), so all loads of
-//     a tile are in flight together;
-//   * the four waves of a workgroup take interleaved 32-key tiles and merge
-//     their (max, sum, O) through LDS at the end with one float4 write per
-//     element and a single barrier;
-//   * splits of a long context write fp32 partials (unnormalised O plus
-//     log2-domain max and sum) that a second kernel merges — the kernel
-//     boundary is what makes them visible across XCDs, at a fraction of the
-//     cost of device-scope fences, which write back and invalidate the whole
-//     L2 of every XCD that executes one.  A sequence that fits one split is
-//     normalised and written directly by the first kernel.
+//     products); V is staged through LDS and read back with gfx950's
+//     transposing LDS read;
+//   * every K/V load of a tile is unconditional (missing keys read a mapped
+//     row), so the compiler's wait counts stay exact across the pipeline.
+//
+// Two bf16 decompositions, chosen by make_plan:
+//   * key-split (verify_attn_ks_kernel): workgroup = (pair, key split), full
+//     head dim; splits of a pair merge in-kernel (the last split to finish
+//     combines the partials, exchanged with agent-scope loads and stores);
+//   * d-sliced (verify_attn_bf16_kernel): workgroup = (pair, head-dim slice,
+//     key split); every slice recomputes the scores and reads the pair's K
+//     through its own L1 (shared in L2); splits, when used, merge in a
+//     second kernel.
+// The fp32 kernel (the 1e-5 contract) uses VALU dot products.
 
 #include "common.h"
 
 namespace {
 
 constexpr int kTile = 32;   // keys per wave iteration
-constexpr int kBf16Waves = 8;  // waves per workgroup (bf16 path)
+constexpr int kBf16Waves = 8;  // waves per workgroup (d-sliced bf16 kernel)
+#ifndef NSV_KS_WAVES
+#define NSV_KS_WAVES 8
+#endif
+constexpr int kKsWaves = NSV_KS_WAVES;  // waves per workgroup of the key-split kernel (two workgroups per CU)
 constexpr int kMaxSplitPages = 1024;  // block-table entries of one split staged in LDS
+// Pairs of the key-split kernel's arrival-counter area at the front of the
+// workspace.  The area has one fixed size, so every call finds its counters
+// at the same place, zero, whatever the previous call's shape was.
+constexpr int kMaxCounterPairs = 16384;
+#ifndef NSV_MAX_STAGES
+#define NSV_MAX_STAGES 4  // deepest key-split pipeline
+#endif
+
+// Pipeline depth of the d-sliced bf16 kernel.  Its slices re-read the pair's
+// K through L1, whose fill rate bounds it, and deeper pipelines only add
+// pressure there: on MI355X at config 2, 2 stages take 20.6 us, 3 21.3 us,
+// 4 23.2 us.  So 2, the floor of the register estimate used for the
+// key-split kernel below.
+constexpr int bf16_stages(int, int, int, bool) { return 2; }
 constexpr float kNegInf = -__builtin_inff();
 
 struct VerifyArgs {
@@ -48,12 +64,25 @@ struct VerifyArgs {
   void* out;
   float* part_ml;    // [B, Hkv, S, Mv, 2]  (running max, running sum), log2 domain
   float* part_o;     // [B, Hkv, S, Mv, D]  unnormalised split outputs
+  unsigned* counters;  // [B, Hkv] splits of the pair done so far (key-split kernel; 0 between calls)
   float scale_log2;  // softmax scale * log2(e)
   int H, Hkv, G, bs_log2, max_blocks, QL, Mv, S, split_tokens, P8, npairs;
-  int dqc;           // head-dim slices per pair (bf16 path)
+  int dqc;           // head-dim slices per pair (d-sliced bf16 kernel)
+  int ks_splits;     // key-split kernel: splits per sequence when split_tokens == 0
 };
 
 __device__ __forceinline__ u32x4 load16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+
+// A float pair as one 64-bit agent-scope (device-coherent) relaxed atomic
+// store / load: coherent across XCDs without cache maintenance instructions.
+__device__ __forceinline__ void store_agent(uint64_t* p, float x, float y) {
+  const uint64_t v = (uint64_t)__float_as_uint(x) | ((uint64_t)__float_as_uint(y) << 32);
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float2 load_agent(const uint64_t* p) {
+  const uint64_t v = __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
+}
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
@@ -65,10 +94,20 @@ __device__ __forceinline__ int context_len(const VerifyArgs& a, int b) {
   return (int)(ctx < 0 ? 0 : (ctx < cap ? ctx : cap));
 }
 
+// Keys per split of a sequence with ctx keys: the caller's fixed split, or
+// (key-split kernel, automatic) ctx spread evenly over ks_splits splits in
+// whole 16-key tiles.
+__device__ __forceinline__ int split_len(const VerifyArgs& a, int ctx) {
+  if (a.split_tokens > 0) return a.split_tokens;
+  const int per = (ctx + a.ks_splits - 1) / a.ks_splits;
+  return per <= 16 ? 16 : (per + 15) & ~15;
+}
+
 // Number of key splits sequence b actually uses (>= 1 so that an empty
 // sequence still gets its rows written).
-__device__ __forceinline__ int splits_for(int ctx, int split_tokens) {
-  return ctx <= split_tokens ? 1 : (ctx + split_tokens - 1) / split_tokens;
+__device__ __forceinline__ int num_splits(const VerifyArgs& a, int ctx) {
+  const int len = split_len(a, ctx);
+  return ctx <= len ? 1 : (ctx + len - 1) / len;
 }
 
 // Workgroup -> (split, pair) with every split of a (sequence, kv-head) pair
@@ -82,7 +121,7 @@ __device__ __forceinline__ void decode_block(const VerifyArgs& a, int& split, in
 }
 
 // ---------------------------------------------------------------------------
-// bf16 path: 4 waves, MFMA 16x16x32.
+// bf16 d-sliced kernel: 8 waves, MFMA 16x16x32.
 // ---------------------------------------------------------------------------
 // Cross-lane reductions over the four lanes c, c+16, c+32, c+48 that hold one
 // query row's statistics, with gfx950's permlane swaps (VALU, no LDS round
@@ -118,8 +157,9 @@ __device__ __forceinline__ uint2 lds_read_tr(const uint16_t* p) {
 // workgroups than pairs — enough to cover the chip without key splits in
 // the common case, which keeps the operator a single kernel.
 //
-// Each wave runs a two-stage register pipeline: tile i+1's K and V loads
-// are in flight while tile i computes; two waves share each SIMD.  Block-
+// Each wave runs an NS-stage register pipeline: the loads of its next NS
+// tiles are in flight while a tile computes (a short context's whole key
+// range is in flight at once); two waves share each SIMD.  Block-
 // table entries of the split are staged in LDS once.  UPAGE (block_size
 // >= 32): a tile lies in one page, whose id is wave-uniform (scalar base
 // address, 32-bit offsets).
@@ -129,7 +169,7 @@ __device__ __forceinline__ uint2 lds_read_tr(const uint16_t* p) {
 // exp2 (results below 2^-126 flush to zero; their weight is negligible, as
 // with the flush-to-zero exp of the reference's Triton kernel).  Tiles with
 // every key present and below every real query row's position skip masking.
-template <int MT, int DH, int DC, bool UPAGE>
+template <int MT, int DH, int DC, bool UPAGE, int NS>
 __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(VerifyArgs a) {
   constexpr int NW = kBf16Waves;
   constexpr int NT = NW * 64;
@@ -188,7 +228,7 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
   const int q0 = a.cu_seqlens_q[b];
   const int qlen = a.cu_seqlens_q[b + 1] - q0;
   __builtin_amdgcn_sched_barrier(0);
-  const int nsplit = splits_for(ctx, a.split_tokens);
+  const int nsplit = num_splits(a, ctx);
   if (split >= nsplit || qlen < 0) return;  // uniform per workgroup
   const int tok_end = min(ctx, range_end);
 #pragma unroll
@@ -261,6 +301,9 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
 
   // Issue every load of wave-tile `it`.  Masked keys read the row of a key
   // that exists (finite data, zero weight), or any mapped row when none does.
+  // Tiles past the split's end have no key and read the pool's first row
+  // (one cached line): every issue has the same loads, so the compiler's
+  // wait counts stay exact across the pipeline.
   auto issue = [&](Tile& T, int it) {
     T.n0 = tok_begin + (it * NW + w) * kTile;
     if constexpr (UPAGE) {
@@ -414,21 +457,21 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
     __builtin_amdgcn_wave_barrier();
   };
 
-  // ---- two-stage pipeline over this wave's tiles
-  Tile A, B;
+  // ---- NS-stage pipeline over this wave's tiles
+  Tile T[NS];
   load_q();
   __builtin_amdgcn_sched_barrier(0);
-  issue(A, 0);
-  issue(B, 1);
+#pragma unroll
+  for (int s = 0; s < NS; ++s) issue(T[s], s);
   __builtin_amdgcn_sched_barrier(0);
   finish_positions();
-  for (int it = 0; it < niter; it += 2) {
-    __builtin_amdgcn_sched_barrier(0);
-    compute(A);
-    issue(A, it + 2);
-    __builtin_amdgcn_sched_barrier(0);
-    compute(B);
-    issue(B, it + 3);
+  for (int it = 0; it < niter; it += NS) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      __builtin_amdgcn_sched_barrier(0);
+      compute(T[s]);
+      issue(T[s], it + s + NS);
+    }
   }
 
   // ---- merge the waves' (max, sum, O) ---------------------------------------
@@ -503,6 +546,390 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
 }
 
 // ---------------------------------------------------------------------------
+// bf16 key-split kernel: workgroup = (pair, key split), full head dim.
+// ---------------------------------------------------------------------------
+// Each workgroup reads only its split's K/V rows, so HBM and every CU see
+// each byte once; a pair's context is cut into num_splits() even splits so
+// that the grid covers the chip, and the merge kernel combines the splits'
+// partials.  (The d-sliced kernel above instead re-reads a pair's K once per
+// head-dim slice through L1; at these shapes that re-read, not arithmetic,
+// bounds it.)
+//
+// Waves take interleaved 16-key tiles.  Per tile:
+//   S^T = K Q^T   v_mfma_f32_16x16x32_bf16, A = K rows straight from HBM
+//                 (lane (g4, c): key c, dims 32 ks + 8 g4 .. +7);
+//   O^T += V^T P^T  v_mfma_f32_16x16x16_bf16: the S^T accumulator (lane
+//                 (g4, c) element i = key 4 g4 + i, query row c) is already
+//                 the B operand P^T; V^T comes from the wave's LDS copy of
+//                 the tile through one transposing read per 16 dims.
+// An NS-stage register pipeline keeps the next NS tiles' loads in flight.
+// The sequence's whole block-table row is fetched in the first round trip
+// (with the context length and query range), so no load waits on another.
+template <int MT, int DH, int NS, int NW>
+__global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyArgs a) {
+  constexpr int NT = NW * 64;
+  constexpr int TK = 16;          // keys per wave tile
+  constexpr int KS = DH / 32;     // k-steps of S^T
+  constexpr int DT = DH / 16;     // 16-dim tiles of O^T
+  constexpr int MP = MT * 16;     // padded query rows
+  constexpr int VCH = DH / 8;     // 16-byte chunks per key row
+  constexpr int KPI = NSV_WAVE / VCH;  // keys per coalesced V load
+  constexpr int VL = TK / KPI;    // V loads per lane per tile
+  constexpr int VSTR = DH + 16;   // staged V row stride (bf16): an odd multiple of 32 bytes
+  constexpr int RSTR = DH + 4;    // merge-region row stride (floats)
+  constexpr int STAGE = NW * TK * VSTR * 2;
+  constexpr int MTILE_BYTES = NW * 16 * RSTR * 4;
+  constexpr int SMEM = STAGE > MTILE_BYTES ? STAGE : MTILE_BYTES;
+
+  __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM];
+  __shared__ int pages[kMaxSplitPages];
+  __shared__ float red_m[NW][MP];
+  __shared__ float red_l[NW][MP];
+  __shared__ float row_l[MP];
+  __shared__ float row_ms[MP];
+  __shared__ int row_pos[MP];
+
+  // ---- workgroup -> (pair, split); every split of a pair on one XCD
+  const int wg = blockIdx.x;
+  const int yy = wg >> 3;
+  const int pair = (yy % a.P8) * 8 + (wg & 7);
+  const int split = yy / a.P8;
+  if (pair >= a.npairs) return;  // grid rounds the pair count up to a multiple of 8
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g4 = lane >> 4, c = lane & 15;
+  const int b = pair / a.Hkv, hk = pair - b * a.Hkv;
+
+  // ---- first round trip: block-table row, context length, query range
+  const int32_t* btrow = a.block_tables + (int64_t)b * a.max_blocks;
+  constexpr int PPT = (kMaxSplitPages + NT - 1) / NT;
+  int pv[PPT];
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) {
+    const int j = tid + i * NT;
+    pv[i] = j < a.max_blocks ? btrow[j] : -1;
+  }
+  const int ctx = context_len(a, b);
+  const int q0 = a.cu_seqlens_q[b];
+  const int qlen = a.cu_seqlens_q[b + 1] - q0;
+  __builtin_amdgcn_sched_barrier(0);
+  const int nsplit = num_splits(a, ctx);
+  if (split >= nsplit || qlen < 0) return;  // uniform per workgroup
+  const int len = split_len(a, ctx);
+  const int kb = split * len;
+  const int ke = min(ctx, kb + len);
+#pragma unroll
+  for (int i = 0; i < PPT; ++i) {
+    const int j = tid + i * NT;
+    if (j < a.max_blocks) pages[j] = pv[i];
+  }
+
+  bf16x8 qB[MT][KS];
+  int qpos[MT];
+  int qmin = 0x7fffffff;
+  auto load_q = [&]() {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = mt * 16 + c;
+      const int g = m / a.QL, t = m - g * a.QL;
+      const bool ok = (m < a.Mv) && (t < qlen);
+      const int row = ok ? q0 + t : 0;
+      const int gg = ok ? g : 0;
+      qpos[mt] = (int)a.positions[row];
+      const bf16_t* qrow = (const bf16_t*)a.q + ((int64_t)row * a.H + hk * a.G + gg) * DH;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) qB[mt][ks] = as_bf16x8(load16(qrow + ks * 32 + g4 * 8));
+    }
+  };
+  auto finish_positions = [&]() {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = mt * 16 + c;
+      const int g = m / a.QL, t = m - g * a.QL;
+      const bool ok = (m < a.Mv) && (t < qlen);
+      qpos[mt] = ok ? qpos[mt] : -1;
+      if (qpos[mt] >= 0) qmin = min(qmin, qpos[mt]);
+      if (w == 0 && g4 == 0) row_pos[m] = qpos[mt];
+    }
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) qmin = min(qmin, __shfl_xor(qmin, o, NSV_WAVE));
+    qmin = __builtin_amdgcn_readfirstlane(qmin);
+  };
+
+  float m_run[MT], l_run[MT];  // running max of raw scores, running sum
+  f32x4 acc[DT][MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    m_run[mt] = kNegInf;
+    l_run[mt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) acc[dt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const float sc = a.scale_log2;
+  const int bs_mask = (1 << a.bs_log2) - 1;
+  const unsigned row_bytes = (unsigned)a.Hkv * DH * 2;  // bytes between consecutive keys of a page
+  const size_t page_bytes = (size_t)row_bytes << a.bs_log2;
+  const char* kbase = (const char*)a.k_cache + hk * DH * 2;
+  const char* vbase = (const char*)a.v_cache + hk * DH * 2;
+  uint16_t* vl = reinterpret_cast<uint16_t*>(smem) + w * TK * VSTR;
+  __syncthreads();  // block-table row visible
+
+  const int ntiles = (ke - kb + TK - 1) / TK;
+  const int niter = (ntiles + NW - 1) / NW;  // same trip count in every wave
+
+  struct Tile {
+    u32x4 k[KS];  // K as the A operand of S^T
+    u32x4 v[VL];  // V rows, coalesced: load j, lane -> (key j * KPI + lane / VCH, chunk lane % VCH)
+    int n0;
+    int nvalid;   // the tile's existing keys are exactly its first nvalid
+  };
+
+  // Issue every load of wave-tile `it` (tiles never cross a page: splits
+  // start on 16-key boundaries and pages hold a power of two >= 16 keys).
+  // Missing keys, and tiles past the split, read a row that exists or the
+  // pool's first row: every issue has the same loads, so the compiler's
+  // wait counts stay exact across the pipeline.
+  auto issue = [&](Tile& T, int it) {
+    T.n0 = kb + (it * NW + w) * TK;
+    int nvalid = min(max(ke - T.n0, 0), TK);
+    int pg = nvalid > 0 ? pages[T.n0 >> a.bs_log2] : -1;
+    pg = __builtin_amdgcn_readfirstlane(pg);
+    if (pg < 0) nvalid = 0;
+    T.nvalid = nvalid;
+    const size_t page_off = (size_t)(pg < 0 ? 0 : pg) * page_bytes;
+    const char* kp = kbase + page_off;
+    const char* vp = vbase + page_off;
+    const unsigned base_key = (unsigned)(T.n0 & bs_mask);
+    {
+      const unsigned off = (base_key + (c < nvalid ? c : 0)) * row_bytes + g4 * 16;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) T.k[ks] = load16(kp + off + ks * 64);
+    }
+#pragma unroll
+    for (int j = 0; j < VL; ++j) {
+      const int r = j * KPI + lane / VCH, ch = lane % VCH;
+      const unsigned off = (base_key + (r < nvalid ? r : 0)) * row_bytes + ch * 16;
+      T.v[j] = load16(vp + off);
+    }
+  };
+
+  auto compute = [&](const Tile& T) {
+    if (T.nvalid == 0) return;  // uniform: nothing of this tile exists
+    f32x4 sacc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      f32x4 sv = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(T.k[ks]), qB[mt][ks], sv, 0, 0, 0);
+      sacc[mt] = sv;
+    }
+    // stage V (this wave's private LDS rows; a wave's LDS ops complete in order)
+#pragma unroll
+    for (int j = 0; j < VL; ++j) {
+      const int r = j * KPI + lane / VCH, ch = lane % VCH;
+      *reinterpret_cast<u32x4*>(vl + r * VSTR + ch * 8) = T.v[j];
+    }
+    // missing keys and keys past a row's position get -inf (exact 0 weight)
+    const bool full = (T.nvalid == TK) && (T.n0 + TK - 1 <= qmin);
+    if (!full) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = g4 * 4 + i;
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          sacc[mt][i] = (r < T.nvalid && T.n0 + r <= qpos[mt]) ? sacc[mt][i] : kNegInf;
+      }
+    }
+    i16x4 pB[MT];
+    float alpha[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      float mx = __builtin_fmaxf(__builtin_fmaxf(sacc[mt][0], sacc[mt][1]), __builtin_fmaxf(sacc[mt][2], sacc[mt][3]));
+      mx = row_max4(mx);
+      const float m_new = fmaxf(m_run[mt], mx);
+      const float nb = (m_new == kNegInf) ? 0.f : -m_new * sc;  // exp2 bias
+      alpha[mt] = __builtin_amdgcn_exp2f(fmaf(m_run[mt], sc, nb));
+      float p[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(fmaf(sacc[mt][i], sc, nb));
+      l_run[mt] = fmaf(l_run[mt], alpha[mt], row_sum4((p[0] + p[1]) + (p[2] + p[3])));
+      m_run[mt] = m_new;
+      // P^T as the B operand, rounded to bf16 like the reference's p.to(v.dtype)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pB[mt][i] = (short)f32_to_bf16_bits(p[i]);
+    }
+    bool moved = false;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) moved |= alpha[mt] != 1.f;
+    if (__ballot(moved)) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) acc[dt][mt] *= alpha[mt];
+    }
+    __builtin_amdgcn_wave_barrier();
+    // O^T += V^T P^T: lane (g4, c) reads V[4 g4 + j][16 dt + c], j = 0..3
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt) {
+      const uint2 vt = lds_read_tr(vl + (g4 * 4 + (c >> 2)) * VSTR + dt * 16 + (c & 3) * 4);
+      const i16x4 vA = __builtin_bit_cast(i16x4, vt);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        acc[dt][mt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vA, pB[mt], acc[dt][mt], 0, 0, 0);
+    }
+    __builtin_amdgcn_wave_barrier();
+  };
+
+  // ---- NS-stage pipeline over this wave's tiles
+  Tile T[NS];
+  load_q();
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int s = 0; s < NS; ++s) issue(T[s], s);
+  __builtin_amdgcn_sched_barrier(0);
+  finish_positions();
+  for (int it = 0; it < niter; it += NS) {
+#pragma unroll
+    for (int s = 0; s < NS; ++s) {
+      __builtin_amdgcn_sched_barrier(0);
+      compute(T[s]);
+      issue(T[s], it + s + NS);
+    }
+  }
+
+  // ---- merge the waves' (max, sum, O) ---------------------------------------
+  if (g4 == 0) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      red_m[w][mt * 16 + c] = m_run[mt];
+      red_l[w][mt * 16 + c] = l_run[mt];
+    }
+  }
+  __syncthreads();  // also: every wave is done with its V staging rows
+  if (tid < MP) {
+    float M = kNegInf;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, red_m[ww][tid]);
+    const float ref = (M == kNegInf) ? 0.f : M;
+    float L = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) L += red_l[ww][tid] * __builtin_amdgcn_exp2f((red_m[ww][tid] - ref) * sc);
+    row_ms[tid] = M == kNegInf ? kNegInf : M * sc;  // partials carry the log2-domain max
+    row_l[tid] = L;
+  }
+  float fac[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = mt * 16 + c;
+    float M = kNegInf;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, red_m[ww][m]);
+    fac[mt] = __builtin_amdgcn_exp2f((m_run[mt] - ((M == kNegInf) ? 0.f : M)) * sc);
+  }
+  float* region = reinterpret_cast<float*>(smem);  // [NW][16][RSTR], one m-tile per pass
+  constexpr int C4 = DH / 4;
+  const int64_t pbase = ((int64_t)pair * a.S + split) * a.Mv;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    __syncthreads();  // staging rows / the previous pass fully read
+    // lane (g4, c) element i of tile (dt, mt) is O[16 mt + c][16 dt + 4 g4 + i]
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+      *reinterpret_cast<f32x4*>(&region[(w * 16 + c) * RSTR + dt * 16 + g4 * 4]) = acc[dt][mt] * fac[mt];
+    __syncthreads();
+    for (int qd = tid; qd < 16 * C4; qd += NT) {
+      const int r = qd / C4, c4 = qd - r * C4;
+      const int m = mt * 16 + r;
+      if (m >= a.Mv) continue;
+      f32x4 o = *reinterpret_cast<const f32x4*>(&region[r * RSTR + c4 * 4]);
+#pragma unroll
+      for (int ww = 1; ww < NW; ++ww) o += *reinterpret_cast<const f32x4*>(&region[(ww * 16 + r) * RSTR + c4 * 4]);
+      if (nsplit == 1) {
+        const int g = m / a.QL, t = m - g * a.QL;
+        if (t >= qlen) continue;
+        const float L = row_l[m];
+        const float inv = (L > 0.f && row_pos[m] >= 0) ? 1.f / L : 0.f;
+        bf16_t* dst = (bf16_t*)a.out + ((int64_t)(q0 + t) * a.H + hk * a.G + g) * DH + c4 * 4;
+        const uint32_t lo = (uint32_t)f32_to_bf16_bits(o[0] * inv) | ((uint32_t)f32_to_bf16_bits(o[1] * inv) << 16);
+        const uint32_t hi = (uint32_t)f32_to_bf16_bits(o[2] * inv) | ((uint32_t)f32_to_bf16_bits(o[3] * inv) << 16);
+        *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+      } else {
+        if (row_pos[m] < 0) o = f32x4{0.f, 0.f, 0.f, 0.f};
+        uint64_t* dst = reinterpret_cast<uint64_t*>(&a.part_o[(pbase + m) * DH + c4 * 4]);
+        store_agent(dst, o[0], o[1]);
+        store_agent(dst + 1, o[2], o[3]);
+      }
+    }
+  }
+  if (nsplit == 1) return;
+
+  // ---- cross-split merge by the pair's last split to finish ------------------
+  // The partials above and the (max, sum) pairs below are agent-scope stores
+  // (written through to the point of coherence of every XCD).  Once all of
+  // them are acknowledged the split counts itself in; the split that counts
+  // last reads every partial back with agent-scope loads, so no cache
+  // write-back or invalidation of a whole L2 is needed.
+  if (tid < a.Mv) {
+    uint64_t* dst = reinterpret_cast<uint64_t*>(&a.part_ml[(pbase + tid) * 2]);
+    store_agent(dst, row_pos[tid] >= 0 ? row_ms[tid] : kNegInf, row_pos[tid] >= 0 ? row_l[tid] : 0.f);
+  }
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  __shared__ int is_last;
+  if (tid == 0)
+    is_last = __hip_atomic_fetch_add(&a.counters[pair], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+              (unsigned)(nsplit - 1);
+  __syncthreads();
+  if (!is_last) return;
+  if (tid == 0) __hip_atomic_store(&a.counters[pair], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  constexpr int C2 = DH / 2;
+  constexpr int CH = 8;  // splits per round trip
+  const int64_t base0 = (int64_t)pair * a.S * a.Mv;  // row 0 of split 0
+  for (int qd = tid; qd < a.Mv * C2; qd += NT) {
+    const int m = qd / C2, c2 = qd - m * C2;
+    const int g = m / a.QL, t = m - g * a.QL;
+    if (t >= qlen) continue;
+    float M = kNegInf, den = 0.f, n0 = 0.f, n1 = 0.f;
+    for (int s0 = 0; s0 < nsplit; s0 += CH) {
+      float ms[CH], ls[CH], o0[CH], o1[CH];
+#pragma unroll
+      for (int j = 0; j < CH; ++j) {
+        const int sp = s0 + j < nsplit ? s0 + j : s0;
+        const int64_t r = base0 + (int64_t)sp * a.Mv + m;
+        const float2 ml = load_agent(reinterpret_cast<const uint64_t*>(&a.part_ml[r * 2]));
+        const float2 ov = load_agent(reinterpret_cast<const uint64_t*>(&a.part_o[r * DH + c2 * 2]));
+        ms[j] = s0 + j < nsplit ? ml.x : kNegInf;
+        ls[j] = ml.y;
+        o0[j] = ov.x;
+        o1[j] = ov.y;
+      }
+      float Mn = M;
+#pragma unroll
+      for (int j = 0; j < CH; ++j) Mn = fmaxf(Mn, ms[j]);
+      if (Mn == kNegInf) continue;  // no key of this row so far
+      const float rs = exp2f(M - Mn);  // M = -inf: 0 (nothing accumulated yet)
+      den *= rs;
+      n0 *= rs;
+      n1 *= rs;
+#pragma unroll
+      for (int j = 0; j < CH; ++j) {
+        const float wgt = exp2f(ms[j] - Mn);  // -inf (absent split, row without keys): 0
+        den = fmaf(wgt, ls[j], den);
+        n0 = fmaf(wgt, o0[j], n0);
+        n1 = fmaf(wgt, o1[j], n1);
+      }
+      M = Mn;
+    }
+    const float inv = den > 0.f ? 1.f / den : 0.f;
+    bf16_t* dst = (bf16_t*)a.out + ((int64_t)(q0 + t) * a.H + hk * a.G + g) * DH + c2 * 2;
+    *reinterpret_cast<uint32_t*>(dst) =
+        (uint32_t)f32_to_bf16_bits(n0 * inv) | ((uint32_t)f32_to_bf16_bits(n1 * inv) << 16);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // fp32 path: one wave per workgroup, VALU dot products (exact fp32 math, the
 // 1e-5 contract).  Lane = key for Q.K, lane = head dim for P.V.
 // ---------------------------------------------------------------------------
@@ -520,7 +947,7 @@ __global__ __launch_bounds__(64) void verify_attn_f32_kernel(VerifyArgs a) {
   const int lane = threadIdx.x;
   const int b = pair / a.Hkv, hk = pair - b * a.Hkv;
   const int ctx = context_len(a, b);
-  const int nsplit = splits_for(ctx, a.split_tokens);
+  const int nsplit = num_splits(a, ctx);
   if (split >= nsplit) return;
   const int tok_begin = split * a.split_tokens;
   const int tok_end = min(ctx, tok_begin + a.split_tokens);
@@ -638,50 +1065,65 @@ __global__ __launch_bounds__(64) void verify_attn_f32_kernel(VerifyArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Split merge: one workgroup per (query row of the group, pair), one lane
-// per head dim.  The splits' (max, sum) pairs are staged in LDS (dynamic,
-// 2 * S floats), then every lane has all of its nsplit partial loads in
-// flight at once.
+// Split merge: one workgroup per (pair, 4 query rows of the group), 64 lanes
+// per row, D/64 head dims per lane.  Each lane loads its row's (max, sum)
+// and its dims of every split's partial together, 8 splits per round trip,
+// and folds them with a running max:
+//   out = sum_s 2^(m_s - M) o_s / sum_s 2^(m_s - M) l_s.
 // ---------------------------------------------------------------------------
-template <typename OutT>
-__global__ __launch_bounds__(128) void verify_merge_kernel(VerifyArgs a, int DH) {
-  extern __shared__ float ml_s[];  // [S][2]
-  __shared__ float stat[2];
-  const int m = blockIdx.x, pair = blockIdx.y;
-  if (pair >= a.npairs) return;
+template <typename OutT, int E>
+__global__ __launch_bounds__(256) void verify_merge_kernel(VerifyArgs a) {
+  constexpr int DH = 64 * E;
+  constexpr int CH = 8;  // splits per round trip
+  const int pair = blockIdx.x;
+  const int m = blockIdx.y * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (pair >= a.npairs || m >= a.Mv) return;
   const int b = pair / a.Hkv, hk = pair - b * a.Hkv;
   const int ctx = context_len(a, b);
-  const int nsplit = splits_for(ctx, a.split_tokens);
+  const int nsplit = num_splits(a, ctx);
   if (nsplit <= 1) return;  // written by the attention kernel itself
   const int q0 = a.cu_seqlens_q[b];
   const int qlen = a.cu_seqlens_q[b + 1] - q0;
   const int g = m / a.QL, t = m - g * a.QL;
   if (t >= qlen) return;
   const int64_t base = (int64_t)pair * a.S * a.Mv + m;  // row of split 0
-  for (int s = threadIdx.x; s < nsplit; s += blockDim.x) {
-    const float2 v = *reinterpret_cast<const float2*>(&a.part_ml[(base + (int64_t)s * a.Mv) * 2]);
-    ml_s[2 * s] = v.x;
-    ml_s[2 * s + 1] = v.y;
+  float M = kNegInf, den = 0.f, num[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) num[e] = 0.f;
+  for (int s0 = 0; s0 < nsplit; s0 += CH) {
+    float ms[CH], ls[CH], os[CH][E];
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int sp = s0 + j < nsplit ? s0 + j : s0;
+      const int64_t r = base + (int64_t)sp * a.Mv;
+      const float2 ml = *reinterpret_cast<const float2*>(&a.part_ml[r * 2]);
+      ms[j] = s0 + j < nsplit ? ml.x : kNegInf;
+      ls[j] = ml.y;
+#pragma unroll
+      for (int e = 0; e < E; ++e) os[j][e] = a.part_o[r * DH + e * 64 + lane];
+    }
+    float Mn = M;
+#pragma unroll
+    for (int j = 0; j < CH; ++j) Mn = fmaxf(Mn, ms[j]);
+    if (Mn == kNegInf) continue;  // no key of this row so far
+    const float r = exp2f(M - Mn);  // M = -inf: 0 (nothing accumulated yet)
+    den *= r;
+#pragma unroll
+    for (int e = 0; e < E; ++e) num[e] *= r;
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const float wgt = exp2f(ms[j] - Mn);  // -inf (absent split or no key): 0
+      den = fmaf(wgt, ls[j], den);
+#pragma unroll
+      for (int e = 0; e < E; ++e) num[e] = fmaf(wgt, os[j][e], num[e]);
+    }
+    M = Mn;
   }
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    float M = kNegInf;
-    for (int s = 0; s < nsplit; ++s) M = fmaxf(M, ml_s[2 * s]);
-    const float ref = (M == kNegInf) ? 0.f : M;
-    float L = 0.f;
-    for (int s = 0; s < nsplit; ++s) L += ml_s[2 * s + 1] * exp2f(ml_s[2 * s] - ref);
-    stat[0] = ref;
-    stat[1] = L > 0.f ? 1.f / L : 0.f;
-  }
-  __syncthreads();
-  const int d = threadIdx.x;
-  if (d >= DH) return;
-  const float ref = stat[0];
-  float o = 0.f;
-#pragma unroll 16
-  for (int s = 0; s < nsplit; ++s)
-    o += exp2f(ml_s[2 * s] - ref) * a.part_o[(base + (int64_t)s * a.Mv) * DH + d];
-  ((OutT*)a.out)[((int64_t)(q0 + t) * a.H + hk * a.G + g) * DH + d] = (OutT)(o * stat[1]);
+  const float inv = den > 0.f ? 1.f / den : 0.f;
+  OutT* dst = (OutT*)a.out + ((int64_t)(q0 + t) * a.H + hk * a.G + g) * DH;
+#pragma unroll
+  for (int e = 0; e < E; ++e) dst[e * 64 + lane] = (OutT)(num[e] * inv);
 }
 
 // ---------------------------------------------------------------------------
@@ -705,6 +1147,8 @@ __global__ __launch_bounds__(256) void store_kv_kernel(const u32x4* __restrict__
 // ---------------------------------------------------------------------------
 struct Plan {
   int G, QL, Mv, MT, split, S, dqc;
+  int ks;         // 1: key-split kernel, 0: d-sliced kernel (bf16)
+  int ks_splits;  // key-split kernel, automatic splits per sequence (split == 0)
 };
 
 int ilog2_exact(int v) {
@@ -746,6 +1190,41 @@ int make_plan(int B, int H, int Hkv, int D, int block_size, int max_blocks, int 
   const int64_t page_cap = ((int64_t)(kMaxSplitPages - 1) * block_size) / 128 * 128;
   int64_t split = kv_split_tokens;
   p->dqc = 1;
+  p->ks = 0;
+  p->ks_splits = 0;
+  // Kernel choice (bf16).  The key-split kernel reads every K/V byte once
+  // per CU but pays about three memory round trips to merge a pair's splits;
+  // the d-sliced kernel needs no cross-workgroup merge but re-reads the
+  // pair's K through every slice's L1, whose fill rate (~25 GB/s per CU)
+  // then bounds it.  Measured on MI355X: at 64 pairs x ~1.25k keys the two
+  // are within 5% (d-sliced ahead); at 128 pairs x 16k-32k keys the
+  // key-split kernel is 2x faster.  So key-split when the pairs fill the
+  // chip without splits, or when a table holds >= 4096 keys.
+  const int64_t ks_slots = (int64_t)device_cus() * (8 / kKsWaves);  // resident workgroups
+  const bool ks_fits = p->MT <= 3 && block_size >= 16 && max_blocks <= kMaxSplitPages &&
+                       (pairs <= kMaxCounterPairs || (kv_split_tokens == 0 && pairs >= ks_slots));
+  const bool ks_wins = kv_split_tokens > 0 || pairs >= ks_slots || max_ctx >= 4096;
+  if (dtype == NSV_BF16 && ks_fits && ks_wins) {
+    // key-split kernel: each sequence's keys evenly over about CUs / pairs
+    // splits (none when the pairs alone cover the chip), or the caller's
+    // fixed split length
+    p->ks = 1;
+    if (split == 0) {
+      int64_t S = pairs > 0 ? (ks_slots + pairs / 2) / pairs : 1;
+      const int64_t max_tiles = (max_ctx + 15) / 16;
+      if (S > max_tiles) S = max_tiles;
+      if (S > 64) S = 64;
+      if (S < 1 || pairs > kMaxCounterPairs) S = 1;
+      p->ks_splits = (int)S;
+      p->split = 0;
+      p->S = (int)S;
+    } else {
+      p->split = (int)split;
+      p->S = (int)((max_ctx + split - 1) / split);
+    }
+    if (p->S > 8192) return NSV_ERR_UNSUPPORTED;  // the merge stages 2 * S floats in LDS
+    return NSV_OK;
+  }
   if (dtype == NSV_BF16) {
     const int cus = device_cus();
     // widest head-dim slice whose double-buffered K/V tiles and accumulators
@@ -777,39 +1256,71 @@ int make_plan(int B, int H, int Hkv, int D, int block_size, int max_blocks, int 
   return NSV_OK;
 }
 
-// Workspace: [part_ml, 256-byte aligned][part_o].
+// Workspace: [per-pair counters, 256-byte aligned][part_ml, 256-byte aligned][part_o].
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+size_t counter_bytes(int, int) { return (size_t)kMaxCounterPairs * sizeof(unsigned); }
 
 size_t ml_bytes(int B, int Hkv, const Plan& p) { return align256((size_t)B * Hkv * p.S * p.Mv * 2 * sizeof(float)); }
 
 size_t workspace_bytes_for(int B, int Hkv, int D, const Plan& p) {
   if (p.S <= 1) return 0;
-  return ml_bytes(B, Hkv, p) + (size_t)B * Hkv * p.S * p.Mv * (size_t)D * sizeof(float);
+  return counter_bytes(B, Hkv) + ml_bytes(B, Hkv, p) + (size_t)B * Hkv * p.S * p.Mv * (size_t)D * sizeof(float);
 }
 
 template <int MT, int DH, int DC>
 void launch_bf16_dc(const VerifyArgs& a, dim3 grid, hipStream_t s) {
   if (a.bs_log2 >= 5)
-    hipLaunchKernelGGL((verify_attn_bf16_kernel<MT, DH, DC, true>), grid, dim3(kBf16Waves * 64), 0, s, a);
+    hipLaunchKernelGGL((verify_attn_bf16_kernel<MT, DH, DC, true, bf16_stages(MT, DH, DC, true)>), grid, dim3(kBf16Waves * 64), 0, s, a);
   else
-    hipLaunchKernelGGL((verify_attn_bf16_kernel<MT, DH, DC, false>), grid, dim3(kBf16Waves * 64), 0, s, a);
+    hipLaunchKernelGGL((verify_attn_bf16_kernel<MT, DH, DC, false, bf16_stages(MT, DH, DC, false)>), grid, dim3(kBf16Waves * 64), 0, s, a);
+}
+
+// Pipeline depth of the key-split kernel: as many K/V tiles in flight per
+// wave as the 256 VGPRs of a two-waves-per-SIMD launch hold without
+// spilling.  The estimate (VGPRs = 20 + MT * (per query m-tile) + NS * (per
+// tile)) matches the compiler's counts for every instantiation to within a
+// few registers.
+constexpr int ks_stages(int MT, int DH) {
+  const int KS = DH / 32, DT = DH / 16, VL = 16 / (64 / (DH / 8));
+  const int fixed = 20 + MT * (KS * 4 + DT * 4 + 8);
+  const int ns = (256 - fixed) / (4 * KS + 4 * VL);
+  return ns < 2 ? 2 : (ns > NSV_MAX_STAGES ? NSV_MAX_STAGES : ns);
 }
 
 template <int MT>
-void launch_bf16(const VerifyArgs& a, int D, dim3 grid, hipStream_t s) {
-  const int dc = D / a.dqc;  // the plan keeps dc at 32, or 64 for MT <= 2
-  if constexpr (MT <= 2) {
-    if (D == 128) {
-      if (dc == 32) launch_bf16_dc<MT, 128, 32>(a, grid, s);
-      else launch_bf16_dc<MT, 128, 64>(a, grid, s);
-    } else {
-      if (dc == 32) launch_bf16_dc<MT, 64, 32>(a, grid, s);
-      else launch_bf16_dc<MT, 64, 64>(a, grid, s);
-    }
-  } else {
+int launch_ks(const VerifyArgs& a, int D, dim3 grid, hipStream_t s) {
+  if constexpr (MT <= 3) {
+    constexpr int NW = kKsWaves;
+    if (D == 128)
+      hipLaunchKernelGGL((verify_attn_ks_kernel<MT, 128, ks_stages(MT, 128), NW>), grid, dim3(NW * 64), 0, s, a);
+    else
+      hipLaunchKernelGGL((verify_attn_ks_kernel<MT, 64, ks_stages(MT, 64), NW>), grid, dim3(NW * 64), 0, s, a);
+    return NSV_OK;
+  }
+  return NSV_ERR_UNSUPPORTED;
+}
+
+// Head-dim slice width dc = D / dqc must be one the kernels are built for
+// (32, or 64 when MT <= 2): the grid's dq index times DC must stay inside
+// the head, so any other slicing is refused before launch.
+template <int MT>
+int launch_bf16(const VerifyArgs& a, int D, dim3 grid, hipStream_t s) {
+  if (a.dqc <= 0 || D % a.dqc) return NSV_ERR_UNSUPPORTED;
+  const int dc = D / a.dqc;
+  if (dc == 32) {
     if (D == 128) launch_bf16_dc<MT, 128, 32>(a, grid, s);
     else launch_bf16_dc<MT, 64, 32>(a, grid, s);
+    return NSV_OK;
   }
+  if constexpr (MT <= 2) {
+    if (dc == 64) {
+      if (D == 128) launch_bf16_dc<MT, 128, 64>(a, grid, s);
+      else launch_bf16_dc<MT, 64, 64>(a, grid, s);
+      return NSV_OK;
+    }
+  }
+  return NSV_ERR_UNSUPPORTED;
 }
 
 template <int MT>
@@ -868,8 +1379,9 @@ int nsv_verify_attention(void* out, const void* q, const void* k_cache, const vo
   a.positions = positions;
   a.out = out;
   char* ws = (char*)workspace;
-  a.part_ml = need ? (float*)ws : nullptr;
-  a.part_o = need ? (float*)(ws + ml_bytes(B, Hkv, p)) : nullptr;
+  a.counters = need ? (unsigned*)ws : nullptr;
+  a.part_ml = need ? (float*)(ws + counter_bytes(B, Hkv)) : nullptr;
+  a.part_o = need ? (float*)(ws + counter_bytes(B, Hkv) + ml_bytes(B, Hkv, p)) : nullptr;
   a.scale_log2 = scale * 1.4426950408889634f;
   a.H = H;
   a.Hkv = Hkv;
@@ -883,16 +1395,25 @@ int nsv_verify_attention(void* out, const void* q, const void* k_cache, const vo
   a.npairs = B * Hkv;
   a.P8 = (B * Hkv + 7) / 8;
   a.dqc = p.dqc;
+  a.ks_splits = p.ks_splits;
 
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid(8 * p.S * a.P8 * p.dqc);
-  if (dtype == NSV_BF16) {
+  if (dtype == NSV_BF16 && p.ks) {
     switch (p.MT) {
-      case 1: launch_bf16<1>(a, D, grid, s); break;
-      case 2: launch_bf16<2>(a, D, grid, s); break;
-      case 3: launch_bf16<3>(a, D, grid, s); break;
-      default: launch_bf16<4>(a, D, grid, s); break;
+      case 1: rc = launch_ks<1>(a, D, grid, s); break;
+      case 2: rc = launch_ks<2>(a, D, grid, s); break;
+      default: rc = launch_ks<3>(a, D, grid, s); break;
     }
+    if (rc != NSV_OK) return rc;
+  } else if (dtype == NSV_BF16) {
+    switch (p.MT) {
+      case 1: rc = launch_bf16<1>(a, D, grid, s); break;
+      case 2: rc = launch_bf16<2>(a, D, grid, s); break;
+      case 3: rc = launch_bf16<3>(a, D, grid, s); break;
+      default: rc = launch_bf16<4>(a, D, grid, s); break;
+    }
+    if (rc != NSV_OK) return rc;
   } else {
     switch (p.MT) {
       case 1: launch_f32<1>(a, D, grid, s); break;
@@ -902,13 +1423,15 @@ int nsv_verify_attention(void* out, const void* q, const void* k_cache, const vo
     }
   }
   rc = nsv_launch_status();
-  if (rc != NSV_OK || p.S <= 1) return rc;
-  const dim3 mgrid(p.Mv, B * Hkv);
-  const size_t msmem = (size_t)p.S * 2 * sizeof(float);
-  if (dtype == NSV_BF16)
-    hipLaunchKernelGGL(verify_merge_kernel<bf16_t>, mgrid, dim3(D), msmem, s, a, D);
-  else
-    hipLaunchKernelGGL(verify_merge_kernel<float>, mgrid, dim3(D), msmem, s, a, D);
+  if (rc != NSV_OK || p.S <= 1 || (dtype == NSV_BF16 && p.ks)) return rc;  // key-split merges in-kernel
+  const dim3 mgrid(B * Hkv, (p.Mv + 3) / 4);
+  if (dtype == NSV_BF16) {
+    if (D == 128) hipLaunchKernelGGL((verify_merge_kernel<bf16_t, 2>), mgrid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((verify_merge_kernel<bf16_t, 1>), mgrid, dim3(256), 0, s, a);
+  } else {
+    if (D == 128) hipLaunchKernelGGL((verify_merge_kernel<float, 2>), mgrid, dim3(256), 0, s, a);
+    else hipLaunchKernelGGL((verify_merge_kernel<float, 1>), mgrid, dim3(256), 0, s, a);
+  }
   return nsv_launch_status();
 }
 

@@ -104,7 +104,7 @@ def paged_attention_verify(
     ws_bytes = int(h.nsv_verify_attention_workspace_size(
         batch_size, num_heads, num_kv_heads, head_dim, block_size, max_num_blocks, qlen_bound, code,
         kv_split_tokens))
-    ws = _lib.workspace(query.device, ws_bytes)
+    ws = _lib.workspace(query.device, ws_bytes, "verify_attention")
     rc = h.nsv_verify_attention(
         out.data_ptr(), query.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
         block_tables.data_ptr(), context_lens.data_ptr(), cu_seqlens_q.data_ptr(), positions.data_ptr(),

@@ -80,7 +80,7 @@ def accept_greedy(target_logits: torch.Tensor, drafts: torch.Tensor, num_drafts:
     h = _lib.lib()
     code = _lib.dtype_code(target_logits.dtype)
     nbytes = int(h.nsv_accept_workspace_size(B, K, V, code, 0))
-    ws = _lib.workspace(dev, nbytes)
+    ws = _lib.workspace(dev, nbytes, "accept")
     rc = h.nsv_accept_greedy(target_logits.data_ptr(), seq_stride, drafts.data_ptr(), num_drafts.data_ptr(), B, K,
                              V, code, out_tokens.data_ptr(), out_len.data_ptr(), _lib.ptr(ws), nbytes,
                              _lib.stream_ptr(dev))
@@ -139,7 +139,7 @@ def accept_stochastic(target_logits: torch.Tensor, drafts: torch.Tensor, num_dra
     h = _lib.lib()
     code = _lib.dtype_code(target_logits.dtype)
     nbytes = int(h.nsv_accept_workspace_size(B, K, V, code, 1))
-    ws = _lib.workspace(dev, nbytes)
+    ws = _lib.workspace(dev, nbytes, "accept")
     rc = h.nsv_accept_stochastic(
         target_logits.data_ptr(), target_seq_stride, _lib.ptr(draft_logits), draft_seq_stride, draft_row_stride,
         drafts.data_ptr(), num_drafts.data_ptr(), temperature.data_ptr(), _lib.ptr(uniforms), noise.data_ptr(), B, K,

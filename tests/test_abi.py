@@ -59,12 +59,24 @@ def test_workspace_size_matches_split_plan():
     h = _lib.lib()
     # config 2 with 128-key splits: 6 pages x 256 keys -> 12 splits of 18 rows: (max, sum) pairs
     # padded to 256 bytes, then 128-float partial rows
+    # (a fixed 64 KiB area of per-pair arrival counters first)
     pad = lambda x: (x + 255) // 256 * 256
     rows = 8 * 8 * 12 * 18
-    assert h.nsv_verify_attention_workspace_size(8, 16, 8, 128, 256, 6, 9, 1, 128) == pad(rows * 8) + rows * 512
-    # automatic plan for config 2: 64 (sequence, kv-head) pairs x 4 head-dim slices fill the
-    # chip, so every sequence is one split and no workspace is needed
+    cnt = 65536
+    assert h.nsv_verify_attention_workspace_size(8, 16, 8, 128, 256, 6, 9, 1, 128) == cnt + pad(rows * 8) + rows * 512
+    # automatic plan for config 2 (6-page tables): the d-sliced kernel, 64 (sequence, kv-head)
+    # pairs x 4 head-dim slices fill the chip without key splits, so no workspace
     assert h.nsv_verify_attention_workspace_size(8, 16, 8, 128, 256, 6, 9, 1, 0) == 0
+    # 16-page tables (4096 keys): the key-split kernel, 4 splits per sequence for 64 pairs on
+    # the 256 CUs a host without a GPU assumes
+    rows = 8 * 8 * 4 * 18
+    assert h.nsv_verify_attention_workspace_size(8, 16, 8, 128, 256, 16, 9, 1, 0) == cnt + pad(rows * 8) + rows * 512
+    # 16 sequences x 8 kv heads, 128-page tables (config 4's shape at 16 Q heads): 2 splits each
+    rows = 16 * 8 * 2 * 18
+    assert (h.nsv_verify_attention_workspace_size(16, 16, 8, 128, 256, 128, 9, 1, 0)
+            == cnt + pad(rows * 8) + rows * 512)
+    # 32 sequences: the pairs fill the chip, one split each, no workspace
+    assert h.nsv_verify_attention_workspace_size(32, 16, 8, 128, 256, 6, 9, 1, 0) == 0
     # one split: no workspace
     assert h.nsv_verify_attention_workspace_size(1, 16, 8, 128, 256, 1, 9, 1, 256) == 0
 

@@ -54,12 +54,52 @@ def test_split_sizes_agree_with_oracle(dtype, split):
     assert_close(out, _oracle(vb), dtype, f"split {split}")
 
 
-@pytest.mark.parametrize("dtype", ["bf16", "f32"])
-def test_gqa4_8b_shape(dtype):
-    print(f"case: 32Q/8KV dtype={dtype}", flush=True)
-    vb = synth.verify_batch(22, [900, 1500], [9, 9], num_heads=32, num_kv_heads=8, dtype=dtype)
+@pytest.mark.parametrize("dtype,max_blocks", [("bf16", None), ("f32", None), ("bf16", 24)])
+def test_gqa4_8b_shape(dtype, max_blocks):
+    # 36 rows of the 4-head group: three 16-row m-tiles (d-sliced kernel for
+    # the 6-page table, key-split kernel for the 24-page one)
+    print(f"case: 32Q/8KV dtype={dtype} max_blocks={max_blocks}", flush=True)
+    vb = synth.verify_batch(22, [900, 1500], [9, 9], num_heads=32, num_kv_heads=8, dtype=dtype,
+                            max_blocks=max_blocks)
     out = _gpu(vb, max_q_len=9)
     assert_close(out, _oracle(vb), dtype, "gqa4")
+
+
+@pytest.mark.parametrize("max_blocks", [None, 16])
+def test_small_batch_many_key_splits(max_blocks):
+    # few (sequence, kv head) pairs: each context is cut into many short
+    # splits (some sequences shorter than one split per CU share); a 5-page
+    # table takes the d-sliced kernel and its merge kernel, a 16-page table
+    # (4096 keys) the key-split kernel and its in-kernel merge
+    print(f"case: b4 bf16 short and long contexts, max_blocks={max_blocks}", flush=True)
+    vb = synth.verify_batch(27, [1, 17, 300, 1248], [1, 9, 9, 9], dtype="bf16", max_blocks=max_blocks)
+    out = _gpu(vb, max_q_len=9)
+    assert_close(out, _oracle(vb), "bf16", "many splits")
+
+
+def test_workspace_reuse_across_shapes():
+    # calls of different batch sizes (different split plans and partial
+    # layouts) share one workspace; the key-split merge's arrival counters
+    # must come back to zero after each
+    print("case: workspace reuse b8 -> b24 -> b2 -> b8", flush=True)
+    batches = [(8, 30), (24, 31), (2, 32), (8, 30)]
+    for batch, seed in batches:
+        ctx = [int(x) for x in synth.randint(seed, 1, batch, 100, 900)]
+        # 64-page tables (4096 keys): the key-split kernel
+        vb = synth.verify_batch(seed, ctx, [9] * batch, dtype="bf16", block_size=64, max_blocks=64)
+        out = _gpu(vb, max_q_len=9)
+        assert_close(out, _oracle(vb), "bf16", f"reuse b{batch}")
+
+
+@pytest.mark.parametrize("batch,bs,qlen", [(16, 256, 9), (32, 16, 9), (20, 64, 5)])
+def test_wide_batches_use_64_dim_slices(batch, bs, qlen):
+    # >= 128 (sequence, kv head) pairs fill the chip with two 64-dim slices
+    # per pair (the 32-dim slicing of smaller batches is covered above)
+    print(f"case: wide batch={batch} block_size={bs} q_len={qlen}", flush=True)
+    ctx = [int(x) for x in synth.randint(26, batch, batch, 40, 700)]
+    vb = synth.verify_batch(26 + batch, ctx, [qlen] * batch, block_size=bs, dtype="bf16")
+    out = _gpu(vb, max_q_len=qlen)
+    assert_close(out, _oracle(vb), "bf16", f"wide b{batch}")
 
 
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
