@@ -61,10 +61,13 @@ const char* nsv_error_string(int code);
  * Supported: D in {64, 128}; H % Hkv == 0; (H/Hkv)*max_q_len <= 64;
  * block_size a power of two.
  * Workspace: nsv_verify_attention_workspace_size() bytes (0 when every
- * sequence fits one split) of fp32 split partials, no initialisation
- * needed; calls that share a workspace must not run concurrently.  A call
- * is one kernel, or two when some sequence spans several key splits (the
- * second merges the splits).
+ * sequence fits one split): a 64 KiB area of per-(sequence, kv head)
+ * arrival counters, then fp32 split partials.  The counter area must be
+ * zero before a workspace's first call; every call leaves it zero (a
+ * zero-filled allocation is enough).  Calls that share a workspace must not
+ * run concurrently.  A call is one kernel (the key-split kernel merges its
+ * splits itself), or two when the d-sliced kernel splits a sequence's keys
+ * (the second merges the splits).
  */
 size_t nsv_verify_attention_workspace_size(int B, int H, int Hkv, int D,
                                            int block_size, int max_blocks,
@@ -115,24 +118,49 @@ int nsv_accept_greedy(const void* target_logits, int64_t target_seq_stride,
 /*
  * Stochastic acceptance.  temperature [B] fp32: a sequence with
  * temperature <= 1e-6 is accepted greedily (rejection_sampler.py:95).
- * draft_logits NULL: n-gram mode (:75-85): every row 0..num_drafts[b] is
- * sampled and drafts are kept while they equal the samples; noise is
- * [B, K+1, V].  Otherwise model mode (:51-73): draft row i of sequence b at
- * (b*draft_seq_stride + i*draft_row_stride)*V; uniforms [B, K] fp32 decide
- * u < min(1, p_t/p_d); one multinomial per sequence (the resample of the
- * first rejected row, or the bonus) uses noise [B, V].  Randomness is input:
- * torch.multinomial(p, 1) == argmax(p / q) for q = Exp(1) draws in p's dtype
- * (noise has the logits dtype), so a caller drawing u = rand(K) and then q
- * from the reference's generator reproduces its samples.
+ * A sequence without draft rows (n-gram drafts, :75-85) samples every row
+ * 0..num_drafts[b] and keeps drafts while they equal the samples, from
+ * noise [K+1, V].  A sequence with draft rows (model drafts, :51-73) reads
+ * draft row i at (b*draft_seq_stride + i*draft_row_stride)*V; uniforms
+ * [B, K] fp32 decide u < min(1, p_t/p_d); one multinomial (the resample of
+ * the first rejected row, or the bonus) uses noise [V].
+ *   draft_logits NULL: no sequence has draft rows.
+ *   draft_mode [B] (nullable): 0 marks a sequence without draft rows when
+ *     draft_logits is given (a hybrid drafter's n-gram sequences,
+ *     spec_engine/drafters.py:184-196); NULL: every sequence has them.
+ *   noise: sequence b's noise at b*noise_seq_stride elements; 0 selects
+ *     V when every sequence has draft rows, else (K+1)*V.
+ * Randomness is input: torch.multinomial(p, 1) == argmax(p / q) for
+ * q = Exp(1) draws in p's dtype (noise has the logits dtype), so a caller
+ * drawing u = rand(K) and then q from the reference's generator reproduces
+ * its samples.
  */
 int nsv_accept_stochastic(const void* target_logits, int64_t target_seq_stride,
                           const void* draft_logits, int64_t draft_seq_stride,
-                          int64_t draft_row_stride, const int32_t* drafts,
-                          const int32_t* num_drafts, const float* temperature,
-                          const float* uniforms, const void* noise, int B,
+                          int64_t draft_row_stride, const int32_t* draft_mode,
+                          const int32_t* drafts, const int32_t* num_drafts,
+                          const float* temperature, const float* uniforms,
+                          const void* noise, int64_t noise_seq_stride, int B,
                           int K, int V, int dtype, int32_t* out_tokens,
                           int32_t* out_len, void* workspace,
                           size_t workspace_bytes, void* stream);
+
+/*
+ * Token sampling of the decode / draft forward.
+ * Replaces src/myvllm/layers/sampler.py:14-24 (SamplerLayer.forward): for
+ * row b (at b*row_stride elements of logits, dtype), temperature[b] <= 1e-6
+ * takes argmax(logits); otherwise argmax(softmax(logits / T) / q) with the
+ * quotient and the softmax in fp32 (logits divided by an fp32 tensor
+ * promote to fp32) and q = noise[b, :] fp32 [B, V], the reference's
+ * exponential_(1).clamp_min_(1e-10) draws.  The token goes to
+ * out_tokens[b*out_stride].  row_stride a multiple of V.  Workspace:
+ * nsv_sample_workspace_size(); no initialisation needed.
+ */
+size_t nsv_sample_workspace_size(int B, int V, int dtype);
+int nsv_sample(const void* logits, int64_t row_stride, const float* temperature,
+               const float* noise, int B, int V, int dtype,
+               int32_t* out_tokens, int64_t out_stride, void* workspace,
+               size_t workspace_bytes, void* stream);
 
 /*
  * N-gram (prompt-lookup) drafting on a device-resident token history.
@@ -165,6 +193,31 @@ int nsv_prepare_verify(const int32_t* history, int64_t hist_stride,
                        int B, int K, int64_t* input_ids, int64_t* positions,
                        int64_t* slot_mapping, int64_t* context_lens,
                        void* stream);
+
+/*
+ * Rows of a model drafter's K decode steps, all built in one launch.
+ * Replaces the host staging of src/myvllm/engine/model_runner.py:784-823
+ * (run_draft_steps_gpu).  For an active sequence b with n = hist_len[b]
+ * confirmed tokens, step i feeds the token at position n-1+i (step 0: the
+ * last confirmed token; step i > 0: the draft sampled by step i-1) and
+ * attends keys 0..n-1+i:
+ *   ids0/pos0/slot0 [2B]: step 0's rows, the tokens at n-2 and n-1 (the row
+ *     at n-2 rewrites the draft-cache entry of a last draft that a fully
+ *     accepted round never fed to the drafter; a pad when n < 2);
+ *   positions/slot_mapping/context_lens [K, B] int64: step i's row at
+ *     i*B + b (context n+i; row 0 of positions/slot_mapping is step 0's
+ *     second row).
+ * Inactive sequences get pads (id 0, position -1, slot -1, context 0).
+ * (The reference passes context n+i+1, one key past the fed token;
+ * positions past it hold no entry of this round, so this build uses n+i.)
+ */
+int nsv_prepare_draft(const int32_t* history, int64_t hist_stride,
+                      const int32_t* hist_len, const int32_t* block_tables,
+                      int max_blocks, int block_size, const int32_t* active,
+                      int B, int K, int64_t* ids0, int64_t* pos0,
+                      int64_t* slot0, int64_t* positions,
+                      int64_t* slot_mapping, int64_t* context_lens,
+                      void* stream);
 
 /*
  * Commit of accepted tokens into the device-resident history.

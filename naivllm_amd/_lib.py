@@ -37,8 +37,12 @@ SIGNATURES: dict[str, tuple] = {
     "nsv_accept_greedy": (
         _c_int, [_c_vp, _c_i64, _c_vp, _c_vp] + [_c_int] * 4 + [_c_vp, _c_vp, _c_vp, _c_size, _c_vp]),
     "nsv_accept_stochastic": (
-        _c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_i64] + [_c_vp] * 5 + [_c_int] * 4
+        _c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_i64] + [_c_vp] * 6 + [_c_i64] + [_c_int] * 4
         + [_c_vp, _c_vp, _c_vp, _c_size, _c_vp]),
+    "nsv_sample_workspace_size": (_c_size, [_c_int] * 3),
+    "nsv_sample": (_c_int, [_c_vp, _c_i64, _c_vp, _c_vp] + [_c_int] * 3 + [_c_vp, _c_i64, _c_vp, _c_size, _c_vp]),
+    "nsv_prepare_draft": (
+        _c_int, [_c_vp, _c_i64, _c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_int, _c_int] + [_c_vp] * 7),
     "nsv_ngram_draft": (_c_int, [_c_vp, _c_vp, _c_i64] + [_c_int] * 4 + [_c_vp, _c_vp, _c_vp]),
     "nsv_prepare_verify": (
         _c_int, [_c_vp, _c_i64] + [_c_vp] * 4 + [_c_int, _c_int, _c_vp, _c_int, _c_int] + [_c_vp] * 5),

@@ -193,8 +193,12 @@ struct StochArgs {
   const int32_t* num_drafts; // [B]
   const float* temperature;  // [B]
   const float* uniforms;     // [B, K]
-  const void* noise;         // draft rows: [B, V]; none: [B, K+1, V]
+  const void* noise;         // sequence b's noise at b * q_seq: [V] (draft rows) or [K+1, V] (none)
+  const int32_t* row_mode;   // nullable [B]: 0 = sequence b has no draft rows (n-gram mode)
+  int64_t q_seq;
   int B, K, V, dtype, nch;
+  int cdtype;                // dtype results are rounded to (the logits dtype, or fp32 for the sampler)
+  int ndtype;                // dtype of the noise
   // workspace
   float* st_max;     // [B, 2K+1, nch]  chunk max of z = x / T
   double* st_sum;    // [B, 2K+1, nch]  chunk sum of exp(z - chunk max)
@@ -206,18 +210,27 @@ struct StochArgs {
   int32_t* acc;      // [B, K+1] accepted prefix
   double* res_sum;   // [B, nch, 2]  chunk sums of the residual and of p_t
   uint64_t* smp_key; // [B, K+1, nch] chunk argmax of prob / q
-  int32_t* out_tokens;
+  int32_t* out_tokens;       // sequence b's tokens at b * out_seq
+  int64_t out_seq;
   int32_t* out_len;
 };
 
 __device__ __forceinline__ bool is_greedy(const StochArgs& a, int b) { return a.temperature[b] <= 1e-6f; }
-__device__ __forceinline__ int kdrafts(const StochArgs& a, int b) { return min(max(a.num_drafts[b], 0), a.K); }
+// sequence b is verified against draft rows (min(1, p_t/p_d)) rather than
+// by sampling every target row (n-gram drafts)
+__device__ __forceinline__ bool has_rows(const StochArgs& a, int b) {
+  return a.draft != nullptr && (a.row_mode == nullptr || a.row_mode[b] != 0);
+}
+__device__ __forceinline__ int kdrafts(const StochArgs& a, int b) {
+  return a.K == 0 ? 0 : min(max(a.num_drafts[b], 0), a.K);  // K = 0: the sampler (no drafts)
+}
 __device__ __forceinline__ int64_t trow(const StochArgs& a, int b, int r) { return ((int64_t)b * a.t_seq + r) * a.V; }
 __device__ __forceinline__ int64_t drow(const StochArgs& a, int b, int i) { return ((int64_t)b * a.d_seq + (int64_t)i * a.d_row) * a.V; }
 
-// z = x / T rounded to the dtype (rejection_sampler.py:47, :52)
-__device__ __forceinline__ float scaled(const void* base, int64_t i, float T, int dtype) {
-  return div_dt(load_elem(base, i, dtype), T, dtype);
+// z = x / T rounded to the compute dtype (rejection_sampler.py:47, :52;
+// layers/sampler.py:20 divides by an fp32 tensor, so there it is fp32)
+__device__ __forceinline__ float scaled(const StochArgs& a, const void* base, int64_t i, float T) {
+  return div_dt(load_elem(base, i, a.dtype), T, a.cdtype);
 }
 
 // softmax value round(exp(z - m) / s) of one element
@@ -239,7 +252,7 @@ __global__ __launch_bounds__(kThreads) void stoch_stats_kernel(StochArgs a) {
   const bool greedy = is_greedy(a, b);
   const bool is_draft = r > a.K;
   if (!is_draft && r > kb) return;
-  if (is_draft && (greedy || !a.draft || r - a.K - 1 >= kb)) return;
+  if (is_draft && (greedy || !has_rows(a, b) || r - a.K - 1 >= kb)) return;
   const Chunk c = chunk_of(ch, a.nch, a.V);
   const int64_t slot = (int64_t)rowid * a.nch + ch;
   if (greedy) {
@@ -257,11 +270,11 @@ __global__ __launch_bounds__(kThreads) void stoch_stats_kernel(StochArgs a) {
   const void* src = is_draft ? a.draft : a.target;
   const int64_t base = is_draft ? drow(a, b, r - a.K - 1) : trow(a, b, r);
   float m = -__builtin_inff();
-  for (int64_t v = c.lo + threadIdx.x; v < c.hi; v += kThreads) m = fmaxf(m, scaled(src, base + v, T, a.dtype));
+  for (int64_t v = c.lo + threadIdx.x; v < c.hi; v += kThreads) m = fmaxf(m, scaled(a, src, base + v, T));
   m = block_max_f(m, redf);
   double s = 0.0;
   if (m != -__builtin_inff())
-    for (int64_t v = c.lo + threadIdx.x; v < c.hi; v += kThreads) s += exp((double)scaled(src, base + v, T, a.dtype) - (double)m);
+    for (int64_t v = c.lo + threadIdx.x; v < c.hi; v += kThreads) s += exp((double)scaled(a, src, base + v, T) - (double)m);
   s = block_sum_d(s, redd);
   if (threadIdx.x == 0) {
     a.st_max[slot] = m;
@@ -327,7 +340,7 @@ __global__ __launch_bounds__(64) void stoch_decide_kernel(StochArgs a) {
   // row statistics of the rows this sequence uses
   for (int r = lane; r < R; r += 64) {
     const bool is_draft = r > a.K;
-    if ((!is_draft && r > kb) || (is_draft && (!a.draft || r - a.K - 1 >= kb))) continue;
+    if ((!is_draft && r > kb) || (is_draft && (!has_rows(a, b) || r - a.K - 1 >= kb))) continue;
     float M;
     double S;
     combine_row(a, b, r, M, S);
@@ -337,7 +350,7 @@ __global__ __launch_bounds__(64) void stoch_decide_kernel(StochArgs a) {
   __syncthreads();
   if (lane != 0) return;
   dec[3] = 0;
-  if (!a.draft) {
+  if (!has_rows(a, b)) {
     // n-gram mode: every row 0..kb is sampled; decisions come after
     dec[0] = kb;
     dec[1] = 0;
@@ -345,17 +358,17 @@ __global__ __launch_bounds__(64) void stoch_decide_kernel(StochArgs a) {
     return;
   }
   const float T = a.temperature[b];
-  const float floor = round_dt(1e-20f, a.dtype);
+  const float floor = round_dt(1e-20f, a.cdtype);
   int n = 0;
   for (int i = 0; i < kb; ++i) {
     const int32_t d = a.drafts[(int64_t)b * a.K + i];
-    const float pt = prob_of(scaled(a.target, trow(a, b, i) + d, T, a.dtype), a.row_m[(int64_t)b * R + i],
-                             a.row_s[(int64_t)b * R + i], a.dtype);
+    const float pt = prob_of(scaled(a, a.target, trow(a, b, i) + d, T), a.row_m[(int64_t)b * R + i],
+                             a.row_s[(int64_t)b * R + i], a.cdtype);
     const int rd = a.K + 1 + i;
-    float pd = prob_of(scaled(a.draft, drow(a, b, i) + d, T, a.dtype), a.row_m[(int64_t)b * R + rd],
-                       a.row_s[(int64_t)b * R + rd], a.dtype);
+    float pd = prob_of(scaled(a, a.draft, drow(a, b, i) + d, T), a.row_m[(int64_t)b * R + rd],
+                       a.row_s[(int64_t)b * R + rd], a.cdtype);
     pd = fmaxf(pd, floor);                                    // clamp_min(1e-20)
-    const float ratio = fminf(div_dt(pt, pd, a.dtype), 1.0f);  // clamp(max=1)
+    const float ratio = fminf(div_dt(pt, pd, a.cdtype), 1.0f);  // clamp(max=1)
     if (a.uniforms[(int64_t)b * a.K + i] < ratio) {
       acc[n++] = d;
       continue;
@@ -373,11 +386,11 @@ __global__ __launch_bounds__(64) void stoch_decide_kernel(StochArgs a) {
 // p_t and p_d of element v of row r (draft-row mode)
 __device__ __forceinline__ void pt_pd(const StochArgs& a, int b, int r, int64_t v, float T, float& pt, float& pd) {
   const int R = 2 * a.K + 1;
-  pt = prob_of(scaled(a.target, trow(a, b, r) + v, T, a.dtype), a.row_m[(int64_t)b * R + r],
-               a.row_s[(int64_t)b * R + r], a.dtype);
+  pt = prob_of(scaled(a, a.target, trow(a, b, r) + v, T), a.row_m[(int64_t)b * R + r],
+               a.row_s[(int64_t)b * R + r], a.cdtype);
   const int rd = a.K + 1 + r;
-  pd = prob_of(scaled(a.draft, drow(a, b, r) + v, T, a.dtype), a.row_m[(int64_t)b * R + rd],
-               a.row_s[(int64_t)b * R + rd], a.dtype);
+  pd = prob_of(scaled(a, a.draft, drow(a, b, r) + v, T), a.row_m[(int64_t)b * R + rd],
+               a.row_s[(int64_t)b * R + rd], a.cdtype);
 }
 
 // residual = max(p_t - p_d, 0) rounded to the dtype (rejection_sampler.py:63)
@@ -398,7 +411,7 @@ __global__ __launch_bounds__(kThreads) void stoch_residual_kernel(StochArgs a) {
   for (int64_t v = c.lo + threadIdx.x; v < c.hi; v += kThreads) {
     float pt, pd;
     pt_pd(a, b, r, v, T, pt, pd);
-    sr += (double)residual_of(pt, pd, a.dtype);
+    sr += (double)residual_of(pt, pd, a.cdtype);
     sp += (double)pt;
   }
   sr = block_sum_d(sr, red);
@@ -418,7 +431,7 @@ __global__ __launch_bounds__(kThreads) void stoch_sample_kernel(StochArgs a) {
   const int b = rowid / (a.K + 1), r = rowid - b * (a.K + 1);
   const int32_t* dec = a.dec + 4 * b;
   if (dec[3]) return;  // greedy sequence: done
-  const bool ngram = a.draft == nullptr;
+  const bool ngram = !has_rows(a, b);
   if (ngram ? r > dec[0] : r != dec[0]) return;
   const int R = 2 * a.K + 1;
   const float T = a.temperature[b];
@@ -430,27 +443,27 @@ __global__ __launch_bounds__(kThreads) void stoch_sample_kernel(StochArgs a) {
         sr += a.res_sum[((int64_t)b * a.nch + j) * 2 + 0];
         sp += a.res_sum[((int64_t)b * a.nch + j) * 2 + 1];
       }
-      const float Sr = round_dt_d(sr, a.dtype);
+      const float Sr = round_dt_d(sr, a.cdtype);
       sUseRes = Sr > 0.f;  // rejection_sampler.py:64-65
-      sS = Sr > 0.f ? Sr : round_dt_d(sp, a.dtype);
+      sS = Sr > 0.f ? Sr : round_dt_d(sp, a.cdtype);
     }
     __syncthreads();
   }
   const Chunk c = chunk_of(ch, a.nch, a.V);
-  const int64_t nbase = ngram ? ((int64_t)b * (a.K + 1) + r) * a.V : (int64_t)b * a.V;
+  const int64_t nbase = (int64_t)b * a.q_seq + (ngram ? (int64_t)r * a.V : 0);
   uint64_t best = 0;
   for (int64_t v = c.lo + threadIdx.x; v < c.hi; v += kThreads) {
     float p;
     if (resample) {
       float pt, pd;
       pt_pd(a, b, r, v, T, pt, pd);
-      p = div_dt(sUseRes ? residual_of(pt, pd, a.dtype) : pt, sS, a.dtype);  // :66-67 residual / sum
+      p = div_dt(sUseRes ? residual_of(pt, pd, a.cdtype) : pt, sS, a.cdtype);  // :66-67 residual / sum
     } else {
-      p = prob_of(scaled(a.target, trow(a, b, r) + v, T, a.dtype), a.row_m[(int64_t)b * R + r],
-                  a.row_s[(int64_t)b * R + r], a.dtype);
+      p = prob_of(scaled(a, a.target, trow(a, b, r) + v, T), a.row_m[(int64_t)b * R + r],
+                  a.row_s[(int64_t)b * R + r], a.cdtype);
     }
-    const float q = load_elem(a.noise, nbase + v, a.dtype);
-    const uint64_t k = argmax_key(div_dt(p, q, a.dtype), (uint32_t)v);  // multinomial = argmax(p / q)
+    const float q = load_elem(a.noise, nbase + v, a.ndtype);
+    const uint64_t k = argmax_key(div_dt(p, q, a.cdtype), (uint32_t)v);  // multinomial = argmax(p / q)
     best = k > best ? k : best;
   }
   best = block_max_u64(best, red);
@@ -462,7 +475,7 @@ __global__ __launch_bounds__(64) void stoch_finalize_kernel(StochArgs a) {
   const int b = blockIdx.x, lane = threadIdx.x;
   const int32_t* dec = a.dec + 4 * b;
   const int32_t* acc = a.acc + (int64_t)b * (a.K + 1);
-  int32_t* out = a.out_tokens + (int64_t)b * (a.K + 1);
+  int32_t* out = a.out_tokens + (int64_t)b * a.out_seq;
   __shared__ int32_t smp[kMaxK + 1];
   const int kb = kdrafts(a, b);
   if (dec[3]) {  // greedy
@@ -472,7 +485,7 @@ __global__ __launch_bounds__(64) void stoch_finalize_kernel(StochArgs a) {
     }
     return;
   }
-  const bool ngram = a.draft == nullptr;
+  const bool ngram = !has_rows(a, b);
   for (int r = ngram ? 0 : dec[0]; r <= dec[0]; ++r) {
     uint64_t best = 0;
     for (int ch = lane; ch < a.nch; ch += 64) {
@@ -580,21 +593,61 @@ int nsv_accept_greedy(const void* target_logits, int64_t seq_stride, const int32
   return nsv_launch_status();
 }
 
+}  // extern "C"
+
+namespace {
+
+// Fill the workspace views of `a` and launch the stochastic kernels.
+int launch_stoch(StochArgs& a, const StochLayout& L, char* ws, bool any_rows, hipStream_t s) {
+  a.st_max = (float*)(ws + L.st_max);
+  a.st_sum = (double*)(ws + L.st_sum);
+  a.st_key = (uint64_t*)(ws + L.st_key);
+  a.row_m = (float*)(ws + L.row_m);
+  a.row_s = (double*)(ws + L.row_s);
+  a.dec = (int32_t*)(ws + L.dec);
+  a.acc = (int32_t*)(ws + L.acc);
+  a.res_sum = (double*)(ws + L.res_sum);
+  a.smp_key = (uint64_t*)(ws + L.smp_key);
+  const int B = a.B, K = a.K, nch = a.nch;
+  hipLaunchKernelGGL(stoch_stats_kernel, dim3(B * (2 * K + 1), nch), dim3(kThreads), 0, s, a);
+  int rc = nsv_launch_status();
+  if (rc) return rc;
+  hipLaunchKernelGGL(stoch_decide_kernel, dim3(B), dim3(64), 0, s, a);
+  if ((rc = nsv_launch_status())) return rc;
+  if (any_rows) {
+    hipLaunchKernelGGL(stoch_residual_kernel, dim3(B, nch), dim3(kThreads), 0, s, a);
+    if ((rc = nsv_launch_status())) return rc;
+  }
+  hipLaunchKernelGGL(stoch_sample_kernel, dim3(B * (K + 1), nch), dim3(kThreads), 0, s, a);
+  if ((rc = nsv_launch_status())) return rc;
+  hipLaunchKernelGGL(stoch_finalize_kernel, dim3(B), dim3(64), 0, s, a);
+  return nsv_launch_status();
+}
+
+}  // namespace
+
+extern "C" {
+
 int nsv_accept_stochastic(const void* target_logits, int64_t target_seq_stride, const void* draft_logits,
-                          int64_t draft_seq_stride, int64_t draft_row_stride, const int32_t* drafts,
-                          const int32_t* num_drafts, const float* temperature, const float* uniforms,
-                          const void* noise, int B, int K, int V, int dtype, int32_t* out_tokens,
-                          int32_t* out_len, void* workspace, size_t workspace_bytes, void* stream) {
+                          int64_t draft_seq_stride, int64_t draft_row_stride, const int32_t* draft_mode,
+                          const int32_t* drafts, const int32_t* num_drafts, const float* temperature,
+                          const float* uniforms, const void* noise, int64_t noise_seq_stride, int B, int K, int V,
+                          int dtype, int32_t* out_tokens, int32_t* out_len, void* workspace, size_t workspace_bytes,
+                          void* stream) {
   if (bad_shape(B, K, V, dtype) || target_seq_stride < K + 1) return NSV_ERR_ARG;
   if (draft_logits && (draft_row_stride < 1 || draft_seq_stride < 0)) return NSV_ERR_ARG;
+  if (draft_mode && !draft_logits) return NSV_ERR_ARG;
   if (B == 0) return NSV_OK;
   if (!target_logits || (!drafts && K > 0) || !num_drafts || !temperature || !noise || !out_tokens || !out_len)
     return NSV_ERR_ARG;
   if (draft_logits && !uniforms && K > 0) return NSV_ERR_ARG;
+  // noise per sequence: [V] when every sequence has draft rows, else [K+1, V]
+  const int64_t q_default = (draft_logits && !draft_mode) ? (int64_t)V : (int64_t)(K + 1) * V;
+  if (noise_seq_stride == 0) noise_seq_stride = q_default;
+  if (noise_seq_stride < q_default) return NSV_ERR_ARG;
   const int nch = choose_nch(B * (2 * K + 1), V);
   const StochLayout L = stoch_layout(B, K, nch);
   if (!workspace || workspace_bytes < L.total) return NSV_ERR_WORKSPACE;
-  char* ws = (char*)workspace;
   StochArgs a;
   a.target = target_logits;
   a.t_seq = target_seq_stride;
@@ -606,36 +659,59 @@ int nsv_accept_stochastic(const void* target_logits, int64_t target_seq_stride, 
   a.temperature = temperature;
   a.uniforms = uniforms;
   a.noise = noise;
+  a.row_mode = draft_mode;
+  a.q_seq = noise_seq_stride;
   a.B = B;
   a.K = K;
   a.V = V;
   a.dtype = dtype;
+  a.cdtype = dtype;
+  a.ndtype = dtype;
   a.nch = nch;
-  a.st_max = (float*)(ws + L.st_max);
-  a.st_sum = (double*)(ws + L.st_sum);
-  a.st_key = (uint64_t*)(ws + L.st_key);
-  a.row_m = (float*)(ws + L.row_m);
-  a.row_s = (double*)(ws + L.row_s);
-  a.dec = (int32_t*)(ws + L.dec);
-  a.acc = (int32_t*)(ws + L.acc);
-  a.res_sum = (double*)(ws + L.res_sum);
-  a.smp_key = (uint64_t*)(ws + L.smp_key);
   a.out_tokens = out_tokens;
+  a.out_seq = K + 1;
   a.out_len = out_len;
-  hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(stoch_stats_kernel, dim3(B * (2 * K + 1), nch), dim3(kThreads), 0, s, a);
-  int rc = nsv_launch_status();
-  if (rc) return rc;
-  hipLaunchKernelGGL(stoch_decide_kernel, dim3(B), dim3(64), 0, s, a);
-  if ((rc = nsv_launch_status())) return rc;
-  if (draft_logits) {
-    hipLaunchKernelGGL(stoch_residual_kernel, dim3(B, nch), dim3(kThreads), 0, s, a);
-    if ((rc = nsv_launch_status())) return rc;
-  }
-  hipLaunchKernelGGL(stoch_sample_kernel, dim3(B * (K + 1), nch), dim3(kThreads), 0, s, a);
-  if ((rc = nsv_launch_status())) return rc;
-  hipLaunchKernelGGL(stoch_finalize_kernel, dim3(B), dim3(64), 0, s, a);
-  return nsv_launch_status();
+  return launch_stoch(a, L, (char*)workspace, draft_logits != nullptr, (hipStream_t)stream);
+}
+
+size_t nsv_sample_workspace_size(int B, int V, int dtype) {
+  if (bad_shape(B, 0, V, dtype)) return 0;
+  return stoch_layout(B, 0, choose_nch(B, V)).total + a256((size_t)B * sizeof(int32_t));
+}
+
+int nsv_sample(const void* logits, int64_t row_stride, const float* temperature, const float* noise, int B, int V,
+               int dtype, int32_t* out_tokens, int64_t out_stride, void* workspace, size_t workspace_bytes,
+               void* stream) {
+  if (bad_shape(B, 0, V, dtype) || row_stride < V || row_stride % V || out_stride < 1) return NSV_ERR_ARG;
+  if (B == 0) return NSV_OK;
+  if (!logits || !temperature || !noise || !out_tokens) return NSV_ERR_ARG;
+  const int nch = choose_nch(B, V);
+  const StochLayout L = stoch_layout(B, 0, nch);
+  if (!workspace || workspace_bytes < nsv_sample_workspace_size(B, V, dtype)) return NSV_ERR_WORKSPACE;
+  StochArgs a;
+  a.target = logits;
+  a.t_seq = row_stride / V;
+  a.draft = nullptr;
+  a.d_seq = 0;
+  a.d_row = 1;
+  a.drafts = nullptr;
+  a.num_drafts = nullptr;
+  a.temperature = temperature;
+  a.uniforms = nullptr;
+  a.noise = noise;
+  a.row_mode = nullptr;
+  a.q_seq = V;
+  a.B = B;
+  a.K = 0;
+  a.V = V;
+  a.dtype = dtype;
+  a.cdtype = NSV_F32;  // logits / (fp32 tensor) promotes to fp32 (layers/sampler.py:20-23)
+  a.ndtype = NSV_F32;
+  a.nch = nch;
+  a.out_tokens = out_tokens;
+  a.out_seq = out_stride;
+  a.out_len = (int32_t*)((char*)workspace + L.total);
+  return launch_stoch(a, L, (char*)workspace, false, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -12,6 +12,9 @@
 // commit: src/myvllm/spec_engine/spec_llm_engine.py:249-291 (_commit: cap by
 //   max_tokens, stop at eos unless ignore_eos, stop at max_model_length,
 //   then the finish test).
+// prepare_draft: the per-step rows of a model drafter's K decode steps
+//   (engine/model_runner.py:784-823, run_draft_steps_gpu), all steps in one
+//   launch.
 
 #include "common.h"
 
@@ -53,6 +56,50 @@ __global__ __launch_bounds__(64) void prepare_verify_kernel(PrepareArgs a) {
   a.input_ids[row] = tok;
   a.positions[row] = pos;
   a.slot_mapping[row] = page < 0 ? -1 : (int64_t)page * a.block_size + pos % a.block_size;
+}
+
+struct DraftPrepArgs {
+  const int32_t* history;    // [B, hstride]
+  int64_t hstride;
+  const int32_t* hist_len;   // [B]
+  const int32_t* block_tables;  // [B, max_blocks] (the draft model's pages)
+  const int32_t* active;     // [B]
+  int B, K, max_blocks, block_size;
+  int64_t* ids0;             // [2B] step 0: the last two confirmed tokens of each sequence
+  int64_t* pos0;             // [2B]
+  int64_t* slot0;            // [2B]
+  int64_t* pos;              // [K, B] position of step i's row (i >= 1)
+  int64_t* slot;             // [K, B]
+  int64_t* ctx;              // [K, B] context length of step i
+};
+
+// Step i of sequence b (n confirmed tokens) feeds the token at position
+// n-1+i and attends keys 0..n-1+i.  Step 0 also re-feeds the token at n-2:
+// after a round whose drafts were all accepted, that token (the last draft)
+// was never fed to the drafter, and this row writes its draft-cache entry.
+__global__ __launch_bounds__(64) void prepare_draft_kernel(DraftPrepArgs a) {
+  const int b = blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= a.B) return;
+  const int n = a.hist_len[b];
+  const bool live = a.active[b] && n > 0;
+  auto slot_of = [&](int pos) -> int64_t {
+    const int page = a.block_tables[(int64_t)b * a.max_blocks + pos / a.block_size];
+    return page < 0 ? -1 : (int64_t)page * a.block_size + pos % a.block_size;
+  };
+  for (int j = 0; j < 2; ++j) {
+    const int pos = n - 2 + j;
+    const bool ok = live && pos >= 0;
+    a.ids0[2 * b + j] = ok ? a.history[(int64_t)b * a.hstride + pos] : 0;
+    a.pos0[2 * b + j] = ok ? pos : -1;
+    a.slot0[2 * b + j] = ok ? slot_of(pos) : -1;
+  }
+  for (int i = 0; i < a.K; ++i) {
+    const int pos = n - 1 + i;
+    const int64_t r = (int64_t)i * a.B + b;
+    a.pos[r] = live ? pos : -1;
+    a.slot[r] = live ? slot_of(pos) : -1;
+    a.ctx[r] = live ? pos + 1 : 0;
+  }
 }
 
 struct CommitArgs {
@@ -117,6 +164,21 @@ int nsv_prepare_verify(const int32_t* history, int64_t hist_stride, const int32_
   PrepareArgs a{history, hist_stride, hist_len, drafts, num_drafts, block_tables, active, B, K, max_blocks,
                 block_size, input_ids, positions, slot_mapping, context_lens};
   hipLaunchKernelGGL(prepare_verify_kernel, dim3(B), dim3(64), 0, (hipStream_t)stream, a);
+  return nsv_launch_status();
+}
+
+int nsv_prepare_draft(const int32_t* history, int64_t hist_stride, const int32_t* hist_len,
+                      const int32_t* block_tables, int max_blocks, int block_size, const int32_t* active, int B,
+                      int K, int64_t* ids0, int64_t* pos0, int64_t* slot0, int64_t* positions,
+                      int64_t* slot_mapping, int64_t* context_lens, void* stream) {
+  if (B < 0 || K < 1 || max_blocks <= 0 || block_size <= 0 || hist_stride <= 0) return NSV_ERR_ARG;
+  if (B == 0) return NSV_OK;
+  if (!history || !hist_len || !block_tables || !active || !ids0 || !pos0 || !slot0 || !positions ||
+      !slot_mapping || !context_lens)
+    return NSV_ERR_ARG;
+  DraftPrepArgs a{history, hist_stride, hist_len, block_tables, active, B, K, max_blocks, block_size,
+                  ids0, pos0, slot0, positions, slot_mapping, context_lens};
+  hipLaunchKernelGGL(prepare_draft_kernel, dim3((B + 63) / 64), dim3(64), 0, (hipStream_t)stream, a);
   return nsv_launch_status();
 }
 

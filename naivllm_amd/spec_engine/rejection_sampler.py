@@ -92,13 +92,17 @@ def accept_stochastic(target_logits: torch.Tensor, drafts: torch.Tensor, num_dra
                       temperature: torch.Tensor, noise: torch.Tensor, uniforms: torch.Tensor | None = None,
                       draft_logits: torch.Tensor | None = None, target_seq_stride: int | None = None,
                       draft_seq_stride: int = 0, draft_row_stride: int = 1,
+                      draft_mode: torch.Tensor | None = None,
                       out_tokens: torch.Tensor | None = None,
                       out_len: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """Batched stochastic acceptance (greedy for sequences whose
     temperature <= 1e-6).  draft_logits None: n-gram mode, noise
     [B, K+1, V]; else model mode: draft row i of sequence b is row
     b*draft_seq_stride + i*draft_row_stride of draft_logits, uniforms
-    [B, K] fp32, noise [B, V].  noise has the logits dtype."""
+    [B, K] fp32, noise [B, V].  draft_mode [B] int32 (with draft_logits)
+    mixes the modes per sequence (0 = n-gram), with noise [B, K+1, V]
+    whose row 0 is a model-mode sequence's one multinomial.  noise has the
+    logits dtype."""
     _check_logits(target_logits, "target_logits")
     dev = target_logits.device
     V = target_logits.shape[-1]
@@ -126,9 +130,15 @@ def accept_stochastic(target_logits: torch.Tensor, drafts: torch.Tensor, num_dra
         uniforms = uniforms.to(device=dev, dtype=torch.float32).contiguous()
     if noise.dtype != target_logits.dtype or not noise.is_contiguous():
         raise ValueError("noise must be contiguous and have the logits dtype")
-    want = B * V if draft_logits is not None else B * (K + 1) * V
-    if noise.numel() != want:
-        raise ValueError(f"noise holds {noise.numel()} values, expected {want}")
+    if draft_mode is not None:
+        if draft_logits is None:
+            raise ValueError("draft_mode selects per-sequence draft rows; draft_logits is missing")
+        draft_mode = _i32(draft_mode, dev)
+        if draft_mode.numel() != B:
+            raise ValueError("draft_mode must hold one flag per sequence")
+    per_seq = V if (draft_logits is not None and draft_mode is None) else (K + 1) * V
+    if noise.numel() != B * per_seq:
+        raise ValueError(f"noise holds {noise.numel()} values, expected {B * per_seq}")
     drafts = _i32(drafts, dev)
     num_drafts = _i32(num_drafts, dev)
     temperature = temperature.to(device=dev, dtype=torch.float32).contiguous()
@@ -142,10 +152,44 @@ def accept_stochastic(target_logits: torch.Tensor, drafts: torch.Tensor, num_dra
     ws = _lib.workspace(dev, nbytes, "accept")
     rc = h.nsv_accept_stochastic(
         target_logits.data_ptr(), target_seq_stride, _lib.ptr(draft_logits), draft_seq_stride, draft_row_stride,
-        drafts.data_ptr(), num_drafts.data_ptr(), temperature.data_ptr(), _lib.ptr(uniforms), noise.data_ptr(), B, K,
-        V, code, out_tokens.data_ptr(), out_len.data_ptr(), _lib.ptr(ws), nbytes, _lib.stream_ptr(dev))
+        _lib.ptr(draft_mode), drafts.data_ptr(), num_drafts.data_ptr(), temperature.data_ptr(), _lib.ptr(uniforms),
+        noise.data_ptr(), per_seq, B, K, V, code, out_tokens.data_ptr(), out_len.data_ptr(), _lib.ptr(ws), nbytes,
+        _lib.stream_ptr(dev))
     _lib.check(rc, "accept_stochastic")
     return out_tokens, out_len
+
+
+def sample(logits: torch.Tensor, temperature: torch.Tensor, noise: torch.Tensor,
+           out: torch.Tensor | None = None) -> torch.Tensor:
+    """The decode sampler of src/myvllm/layers/sampler.py:14-24 on the
+    GPU: logits [B, V] (rows contiguous, any row pitch that is a multiple
+    of V), temperature [B] fp32 (<= 1e-6: argmax), noise [B, V] fp32
+    exponential draws clamped at 1e-10.  Returns / writes int32 tokens
+    [B] (``out`` may be a strided column of a draft buffer)."""
+    _check_logits(logits, "logits")
+    if logits.dim() != 2:
+        raise ValueError("logits must be (batch, vocab)")
+    B, V = logits.shape
+    dev = logits.device
+    if B > 1 and logits.stride(0) % V:
+        raise ValueError("logits row pitch must be a multiple of the vocabulary")
+    pitch = logits.stride(0) if B > 1 else V
+    _check_extent(logits, (B - 1) * pitch + V, "logits")
+    if noise.dtype != torch.float32 or not noise.is_contiguous() or noise.numel() != B * V:
+        raise ValueError("noise must be a contiguous float32 (batch, vocab) tensor")
+    temperature = temperature.to(device=dev, dtype=torch.float32).contiguous()
+    if out is None:
+        out = torch.empty(B, dtype=torch.int32, device=dev)
+    if out.dtype != torch.int32 or out.dim() != 1 or out.numel() != B:
+        raise ValueError("out must be an int32 (batch,) tensor")
+    h = _lib.lib()
+    code = _lib.dtype_code(logits.dtype)
+    nbytes = int(h.nsv_sample_workspace_size(B, V, code))
+    ws = _lib.workspace(dev, nbytes, "sample")
+    rc = h.nsv_sample(logits.data_ptr(), pitch, temperature.data_ptr(), noise.data_ptr(), B, V, code, out.data_ptr(),
+                      out.stride(0) if B > 1 else 1, _lib.ptr(ws), nbytes, _lib.stream_ptr(dev))
+    _lib.check(rc, "sample")
+    return out
 
 
 def draw_randomness(num_drafts: list[int], V: int, dtype: torch.dtype, device, with_draft_rows: bool,

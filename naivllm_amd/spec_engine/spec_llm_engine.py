@@ -2,15 +2,26 @@
 
 Keeps the reference's SpecLLMEngine configuration keys and spec metrics
 (src/myvllm/spec_engine/spec_llm_engine.py:32-102, :305-312):
-``spec_method`` ("ngram", or "none" for plain decoding through the same
-round with drafting off), ``num_speculative_tokens``, ``ngram_min_size``,
-``ngram_max_size``, ``max_num_sequences``, ``max_model_length``,
-``block_size``, ``world_size`` (must be 1, :34-35), ``enforce_eager`` /
-``capture_verify``; ``metrics["spec_decoding"]`` holds ``rounds``,
-``drafted_tokens``, ``accepted_tokens`` and ``fallback_rounds``, cumulative
-over calls as in the reference.  The model is a random-init Qwen3 of the
-shape in ``config["model_config"]`` (no checkpoint loading: :104-137 and
-utils/loader.py fetch weights by name, which this build does not do).
+``spec_method`` ("ngram", "model", "hybrid", or "none" for plain decoding
+through the same round with drafting off), ``num_speculative_tokens``,
+``ngram_min_size``, ``ngram_max_size``, ``max_num_sequences``,
+``max_model_length``, ``block_size``, ``world_size`` (must be 1, :34-35),
+``enforce_eager`` / ``capture_verify``; ``metrics["spec_decoding"]`` holds
+``rounds``, ``drafted_tokens``, ``accepted_tokens`` and ``fallback_rounds``
+(cumulative over calls as in the reference), plus
+``model_fallback_rounds`` / ``model_fallback_seqs`` for a hybrid drafter
+(:305-312).  The target is a random-init Qwen3 of the shape in
+``config["model_config"]``; the model / hybrid drafter a random-init Qwen3
+of ``config["draft_model_config"]`` (Qwen3-0.6B by default) that shares the
+target's vocabulary, pages and block tables (no checkpoint loading: :104-137
+and utils/loader.py fetch weights by name, which this build does not do).
+
+Sampling: a request with temperature <= 1e-6 is decoded greedily; any
+other temperature samples the first token, the model drafts and the
+acceptance (min(1, p_t/p_d) with residual resampling) from torch's device
+generator, seeded from ``config["seed"]``.  Rounds of greedy-only batches
+run the greedy graphs; a batch with a sampled request runs the stochastic
+graphs (built on first use).
 
 Scheduling is a fixed batch: ``generate`` admits up to max_num_sequences
 prompts, prefills them, and runs rounds until every sequence finished;
@@ -30,6 +41,7 @@ from naivllm_amd.engine.sequence import Sequence, SequenceStatus
 from naivllm_amd.engine.verify_round import VerifyRound
 from naivllm_amd.layers.qwen3 import Qwen3Config, Qwen3Verify
 from naivllm_amd.sampling_parameters import SamplingParams
+from naivllm_amd.spec_engine.rejection_sampler import GREEDY_TEMPERATURE, sample
 
 PREFILL_ROWS = 64  # GQA group x query rows one verify-attention call handles
 
@@ -38,8 +50,8 @@ class SpecLLMEngine:
     def __init__(self, config: dict):
         assert config.get("world_size", 1) == 1, "speculative decoding currently supports world_size == 1"
         self.spec_method = config.get("spec_method", "ngram")
-        if self.spec_method not in ("ngram", "none"):
-            raise ValueError(f"spec_method {self.spec_method!r}: this build runs 'ngram' and 'none'")
+        if self.spec_method not in ("ngram", "model", "hybrid", "none"):
+            raise ValueError(f"spec_method {self.spec_method!r}: expected 'ngram', 'model', 'hybrid' or 'none'")
         self.num_speculative_tokens = config.get("num_speculative_tokens", 5)
         self.min_ngram = config.get("ngram_min_size", 2)
         self.max_ngram = config.get("ngram_max_size", 8)
@@ -48,28 +60,57 @@ class SpecLLMEngine:
         self.block_size = config.get("block_size", 256)
         self.eos = config.get("eos_token_id", -1)
         self.device = torch.device(config.get("device", "cuda"))
+        seed = config.get("seed", 0)
+        torch.manual_seed(seed)  # the device generator of the sampled draws
         cfg = config.get("model_config") or Qwen3Config()
-        self.model = Qwen3Verify(cfg, self.device, seed=config.get("seed", 0))
+        self.model = Qwen3Verify(cfg, self.device, seed=seed)
+        self.draft_model = None
+        if self.spec_method in ("model", "hybrid"):
+            dcfg = config.get("draft_model_config") or Qwen3Config.qwen3_0_6b()
+            if dcfg.vocab_size != cfg.vocab_size:
+                raise ValueError("draft and target models must share the tokenizer/vocabulary")
+            self.draft_model = Qwen3Verify(dcfg, self.device, seed=config.get("draft_seed", seed + 1))
         K = self.num_speculative_tokens
         self.history_len = self.max_model_length + K + 1
         self.max_blocks = math.ceil(self.history_len / self.block_size)
         num_blocks = config.get("num_kvcache_blocks", self.max_num_sequences * self.max_blocks)
         self.block_manager = BlockManager(num_blocks, self.block_size)
         self.model.allocate_kv_cache(num_blocks, self.block_size)
-        self.round = VerifyRound(self.model, self.max_num_sequences, K, self.min_ngram, self.max_ngram,
-                                 self.history_len, self.max_blocks, self.eos, draft=self.spec_method != "none")
-        eager = config.get("enforce_eager", False) or not config.get("capture_verify", True)
-        if not eager:
-            self.round.capture()
+        if self.draft_model is not None:
+            self.draft_model.allocate_kv_cache(num_blocks, self.block_size)
+        self.eager = config.get("enforce_eager", False) or not config.get("capture_verify", True)
+        self.rounds: dict[bool, VerifyRound] = {}
+        self._round(False)
         self.spec_stats = {"method": self.spec_method, "num_speculative_tokens": K, "rounds": 0,
                            "drafted_tokens": 0, "accepted_tokens": 0, "fallback_rounds": 0}
+        if self.spec_method == "hybrid":
+            self.spec_stats.update(model_fallback_rounds=0, model_fallback_seqs=0)
+
+    @property
+    def round(self) -> VerifyRound:
+        """The greedy round (built at construction)."""
+        return self._round(False)
+
+    def _round(self, stochastic: bool) -> VerifyRound:
+        """The greedy or the stochastic round, built and captured on first use."""
+        r = self.rounds.get(stochastic)
+        if r is None:
+            r = VerifyRound(self.model, self.max_num_sequences, self.num_speculative_tokens, self.min_ngram,
+                            self.max_ngram, self.history_len, self.max_blocks, self.eos, method=self.spec_method,
+                            draft_model=self.draft_model, stochastic=stochastic)
+            if not self.eager:
+                r.capture()
+            self.rounds[stochastic] = r
+        return r
 
     # ------------------------------------------------------------------ prefill
     @torch.inference_mode()
     def _prefill(self, seq: Sequence) -> int:
-        """KV of the prompt (chunks of prompt rows through the verify forward)
-        and the first completion token (greedy: argmax of the last prompt
-        row), as the reference's prefill + sampler produce it."""
+        """KV of the prompt (chunks of prompt rows through the verify
+        forward; mirrored into the draft model's cache when there is one,
+        spec_llm_engine.py:147-151) and the first completion token, sampled
+        from the last prompt row as the reference's prefill + sampler
+        (layers/sampler.py:14-24) do."""
         dev = self.device
         table = torch.tensor(seq.block_table, dtype=torch.int32, device=dev).unsqueeze(0)
         bs = self.block_size
@@ -77,6 +118,9 @@ class SpecLLMEngine:
         n = len(seq.token_ids)
         cfg = self.model.cfg
         chunk = PREFILL_ROWS // (cfg.num_heads // cfg.num_kv_heads)
+        if self.draft_model is not None:
+            dc = self.draft_model.cfg
+            chunk = min(chunk, PREFILL_ROWS // (dc.num_heads // dc.num_kv_heads))
         for p0 in range(0, n, chunk):
             p1 = min(n, p0 + chunk)
             pos = torch.arange(p0, p1, dtype=torch.int64, device=dev)
@@ -86,7 +130,14 @@ class SpecLLMEngine:
             ctx = torch.tensor([p1], dtype=torch.int64, device=dev)
             cu = torch.tensor([0, p1 - p0], dtype=torch.int32, device=dev)
             logits = self.model.forward(ids, pos, slots, table, ctx, cu, p1 - p0)
-        return int(logits[-1].argmax())
+            if self.draft_model is not None:
+                self.draft_model.forward(ids, pos, slots, table, ctx, cu, p1 - p0)
+        last = logits[-1:]
+        if seq.temperature <= GREEDY_TEMPERATURE:
+            return int(last.argmax())
+        noise = torch.empty(1, last.shape[-1], dtype=torch.float32, device=dev).exponential_(1).clamp_min_(1e-10)
+        temp = torch.full((1,), float(seq.temperature), dtype=torch.float32, device=dev)
+        return int(sample(last, temp, noise)[0])
 
     # ---------------------------------------------------------------- generate
     @torch.inference_mode()
@@ -94,11 +145,8 @@ class SpecLLMEngine:
         if len(prompts) > self.max_num_sequences:
             raise ValueError(f"{len(prompts)} prompts exceed max_num_sequences={self.max_num_sequences}")
         params = sampling_params if isinstance(sampling_params, list) else [sampling_params] * len(prompts)
-        for sp in params:
-            if sp.temperature > 1e-6:
-                raise ValueError("this build's device round accepts greedily (temperature 0)")
         K = self.num_speculative_tokens
-        r = self.round
+        r = self._round(any(sp.temperature > GREEDY_TEMPERATURE for sp in params))
         t0 = time.perf_counter()
         seqs = []
         for slot, (prompt, sp) in enumerate(zip(prompts, params)):
@@ -118,6 +166,7 @@ class SpecLLMEngine:
             r.max_tokens[slot] = sp.max_tokens
             r.max_len[slot] = sp.max_model_length or self.max_model_length
             r.ignore_eos[slot] = int(sp.ignore_eos)
+            r.temperature[slot] = float(sp.temperature)
             r.block_tables[slot].fill_(-1)
             r.block_tables[slot, :len(seq.block_table)] = torch.tensor(seq.block_table, dtype=torch.int32,
                                                                        device=self.device)
@@ -137,13 +186,18 @@ class SpecLLMEngine:
             B = r.bucket_for(max(live) + 1)
             rep = r.run(B)
             rounds += 1
-            act, com, dr = rep[0].tolist(), rep[1].tolist(), rep[2].tolist()
+            act, com, dr, mdl = rep[0].tolist(), rep[1].tolist(), rep[2].tolist(), rep[3].tolist()
             self.spec_stats["rounds"] += 1
+            fallback = 0
             for i in live:
                 if self.spec_method != "none" and dr[i] > 0:
                     self.spec_stats["drafted_tokens"] += dr[i]
                     self.spec_stats["accepted_tokens"] += com[i]
+                    fallback += mdl[i]
                 decode_tokens += com[i]
+            if self.spec_method == "hybrid" and fallback:
+                self.spec_stats["model_fallback_rounds"] += 1
+                self.spec_stats["model_fallback_seqs"] += fallback
             live = [i for i in live if act[i]]
         torch.cuda.synchronize(self.device)
         t_end = time.perf_counter()

@@ -8,7 +8,9 @@ Restates, in float64 numpy with the reference's dtype flow made explicit:
     fed by the batched argmax of spec_llm_engine.py:224-227 and the padded
     row stride of :216-219, :229-243;
   * stochastic acceptance — rejection_sampler.py:38-85 and the temperature
-    dispatch of :87-98.
+    dispatch of :87-98;
+  * token sampling of the decode / draft forward — layers/sampler.py:14-24
+    (SamplerLayer: argmax, or argmax(softmax(logits / T) / q) in fp32).
 
 Randomness is an input.  The reference draws ``torch.rand(K)`` and then one
 ``torch.multinomial`` per sequence; torch implements multinomial(p, 1) as
@@ -167,3 +169,22 @@ def verify(draft_tokens, target_rows, draft_rows=None, temperature: float = 0.0,
         rows = np.asarray(target_rows, dtype=np.float64)
         return verify_greedy(draft_tokens, [argmax_first(r) for r in rows])
     return verify_stochastic(draft_tokens, target_rows, draft_rows, temperature, uniforms, noise, dtype)
+
+
+def sample(logits_row, temperature: float, noise_row) -> int:
+    """layers/sampler.py:14-24 for one row: temperature <= 1e-6 takes the
+    argmax of the logits; otherwise logits / T (a float32 tensor divisor,
+    so the quotient, the softmax and probs / noise are float32) and
+    argmax(probs / noise) with noise the fp32 exponential draws (already
+    clamped at 1e-10 by the caller, :23)."""
+    x = np.asarray(logits_row, dtype=np.float64)
+    if temperature <= 1e-6:
+        return argmax_first(x)
+    p = softmax_rows(x, np.float32(temperature), "f32")[0]
+    return multinomial(p, np.asarray(noise_row, dtype=np.float32), "f32")
+
+
+def sample_rows(logits, temperatures, noise) -> list[int]:
+    """sample() over the rows of logits [B, V] with temperatures [B] and
+    noise [B, V]."""
+    return [sample(logits[b], float(temperatures[b]), noise[b]) for b in range(len(temperatures))]

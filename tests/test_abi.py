@@ -106,8 +106,21 @@ def test_accept_and_ngram_reject_bad_arguments_before_launch():
     assert h.nsv_accept_greedy(1, 9, 1, 1, 0, 8, 100, 1, 1, 1, None, 0, None) == 0   # empty batch
     assert h.nsv_accept_workspace_size(2, 8, 100, 1, 0) > 0
     assert h.nsv_accept_workspace_size(2, 8, 100, 1, 1) > h.nsv_accept_workspace_size(2, 8, 100, 1, 0)
-    # stochastic: model mode needs uniforms
-    assert h.nsv_accept_stochastic(1, 9, 1, 9, 1, 1, 1, 1, None, 1, 2, 8, 100, 1, 1, 1, 1, 1 << 30, None) == -1
+    # stochastic: model mode needs uniforms; a draft_mode array needs draft rows; noise stride too short
+    assert h.nsv_accept_stochastic(1, 9, 1, 9, 1, None, 1, 1, 1, None, 1, 0, 2, 8, 100, 1, 1, 1, 1, 1 << 30,
+                                   None) == -1
+    assert h.nsv_accept_stochastic(1, 9, None, 0, 1, 1, 1, 1, 1, None, 1, 0, 2, 8, 100, 1, 1, 1, 1, 1 << 30,
+                                   None) == -1
+    assert h.nsv_accept_stochastic(1, 9, 1, 9, 1, 1, 1, 1, 1, 1, 1, 100, 2, 8, 100, 1, 1, 1, 1, 1 << 30,
+                                   None) == -1
+    # sampler: row stride not a multiple of V, missing workspace, empty batch
+    assert h.nsv_sample(1, 150, 1, 1, 2, 100, 1, 1, 1, 1, 1 << 20, None) == -1
+    assert h.nsv_sample(1, 100, 1, 1, 2, 100, 1, 1, 1, None, 0, None) == -3
+    assert h.nsv_sample(1, 100, 1, 1, 0, 100, 1, 1, 1, None, 0, None) == 0
+    assert h.nsv_sample_workspace_size(2, 100, 1) > 0
+    # draft-step metadata: K must be >= 1
+    assert h.nsv_prepare_draft(1, 8, 1, 1, 2, 16, 1, 2, 0, 1, 1, 1, 1, 1, 1, None) == -1
+    assert h.nsv_prepare_draft(1, 8, 1, 1, 2, 16, 1, 0, 4, 1, 1, 1, 1, 1, 1, None) == 0
     # n-gram drafter: n range and continuation length
     assert h.nsv_ngram_draft(1, 1, 10, 2, 0, 4, 8, 1, 1, None) == -1
     assert h.nsv_ngram_draft(1, 1, 10, 2, 3, 2, 8, 1, 1, None) == -1

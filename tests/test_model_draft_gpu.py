@@ -1,0 +1,200 @@
+"""The model and hybrid drafters inside the device round: the draft-step
+metadata kernel against the oracle, the drafts against the draft model's own
+greedy decoding, greedy speculative output against plain greedy decoding
+(model and hybrid drafts, graph and eager), one stochastic round against a
+host restatement of the sampler, the acceptance and the commit on the
+round's own logits and random draws, and a drafter identical to the target
+being accepted."""
+
+import numpy as np
+import pytest
+import torch
+
+from naivllm_amd.engine.sequence import Sequence
+from naivllm_amd.engine.verify_round import prepare_draft
+from naivllm_amd.layers.qwen3 import Qwen3Config
+from naivllm_amd.sampling_parameters import SamplingParams
+from naivllm_amd.spec_engine.spec_llm_engine import SpecLLMEngine
+from naivllm_amd.utils import synth
+from oracle import accept as oa
+from oracle import ngram as on
+from oracle import round as orr
+
+pytestmark = pytest.mark.gpu
+
+TARGET = Qwen3Config(vocab_size=2048, hidden_size=256, num_layers=2, num_heads=4, num_kv_heads=2, head_dim=64,
+                     intermediate_size=512, max_position=4096)
+DRAFT = Qwen3Config(vocab_size=2048, hidden_size=128, num_layers=2, num_heads=2, num_kv_heads=1, head_dim=64,
+                    intermediate_size=256, max_position=4096)
+
+
+def i32(x):
+    return torch.tensor(x, dtype=torch.int32, device="cuda")
+
+
+def prompts_with_spans(seed, n, vocab=2048):
+    rng = np.random.default_rng(seed)
+    out = []
+    for b in range(n):
+        spans = [[int(x) for x in rng.integers(0, vocab, 10)] for _ in range(4)]
+        out.append([t for i in range(8 + b) for t in spans[i % 4]] + spans[1][:3])
+    return out
+
+
+def test_prepare_draft_kernel_matches_oracle():
+    print("case: prepare_draft kernel", flush=True)
+    B, K, S, bs, MB = 5, 4, 64, 8, 8
+    hists = [[int(x) for x in synth.randint(b, 90, L, 0, 50)] for b, L in enumerate([10, 1, 31, 0, 17])]
+    active = [1, 1, 1, 1, 0]
+    tables = [[int(x) for x in synth.randperm(b, 91, 64)[:MB]] for b in range(B)]
+    tables[2][3] = -1
+    H = torch.zeros(B, S, dtype=torch.int32)
+    for b, h in enumerate(hists):
+        H[b, :len(h)] = torch.tensor(h, dtype=torch.int32)
+    H = H.cuda()
+    i64 = dict(dtype=torch.int64, device="cuda")
+    ids0, pos0, slot0 = torch.empty(2 * B, **i64), torch.empty(2 * B, **i64), torch.empty(2 * B, **i64)
+    pos, slots, ctx = torch.empty(K * B, **i64), torch.empty(K * B, **i64), torch.empty(K * B, **i64)
+    prepare_draft(H, i32([len(h) for h in hists]), i32(tables), bs, i32(active), K, ids0, pos0, slot0, pos, slots,
+                  ctx)
+    w_ids0, w_pos0, w_slot0, w_pos, w_slots, w_ctx = orr.draft_rows(hists, tables, bs, K, active)
+    assert (ids0.tolist(), pos0.tolist(), slot0.tolist()) == (w_ids0, w_pos0, w_slot0)
+    flat = lambda m: [x for row in m for x in row]
+    assert (pos.tolist(), slots.tolist(), ctx.tolist()) == (flat(w_pos), flat(w_slots), flat(w_ctx))
+
+
+def _load(eng, r, hists, max_tokens=100, temps=None):
+    """Admit histories into round slots (prefill included), as generate does."""
+    for b, h in enumerate(hists):
+        s = Sequence(h, SamplingParams(temperature=temps[b] if temps else 0.0))
+        eng.block_manager.allocate(s)
+        eng.block_manager.ensure_capacity(s, len(h) + 64)
+        eng._prefill(s)
+        r.history[b].zero_()
+        r.history[b, :len(h)] = torch.tensor(h, dtype=torch.int32, device="cuda")
+        r.hist_len[b] = len(h)
+        r.prompt_len[b] = len(h) - 2
+        r.max_tokens[b] = max_tokens
+        r.max_len[b] = 0
+        r.ignore_eos[b] = 1
+        r.active[b] = 1
+        r.temperature[b] = temps[b] if temps else 0.0
+        r.block_tables[b].fill_(-1)
+        r.block_tables[b, :len(s.block_table)] = torch.tensor(s.block_table, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+
+
+def test_model_drafts_equal_the_drafters_greedy_decoding():
+    # one eager greedy round: the K drafts of each sequence are the draft model's own greedy continuation
+    print("case: model drafts == drafter greedy decode", flush=True)
+    K = 5
+    hists = [h[:40 + 3 * i] for i, h in enumerate(prompts_with_spans(4, 3))]
+    eng = SpecLLMEngine(dict(model_config=TARGET, draft_model_config=DRAFT, spec_method="model",
+                             num_speculative_tokens=K, max_num_sequences=4, max_model_length=256, block_size=16,
+                             enforce_eager=True, seed=5))
+    r = eng.round
+    _load(eng, r, hists)
+    r.body(len(hists))
+    torch.cuda.synchronize()
+    drafts = [r.drafts[b, :int(r.num_drafts[b])].tolist() for b in range(len(hists))]
+    assert [int(x) for x in r.num_drafts[:len(hists)]] == [K] * len(hists)
+    dm = eng.draft_model
+    # a plain engine whose model has the drafter's shape and seed (the engine seeds its drafter with seed + 1)
+    solo = SpecLLMEngine(dict(model_config=DRAFT, spec_method="none", max_num_sequences=4, max_model_length=256,
+                              block_size=16, enforce_eager=True, seed=5 + 1))
+    for a, b in zip(dm.layers, solo.model.layers):
+        assert torch.equal(a["qkv"], b["qkv"]) and torch.equal(a["down"], b["down"])
+    del eng
+    res = solo.generate(hists, SamplingParams(temperature=0.0, max_tokens=K, ignore_eos=True))
+    assert [o["token_ids"] for o in res["outputs"]] == drafts
+
+
+@pytest.mark.parametrize("method", ["model", "hybrid"])
+def test_greedy_spec_equals_plain_decode(method):
+    print(f"case: greedy {method} spec == plain, graph == eager", flush=True)
+    prompts = prompts_with_spans(7, 3)
+    sp = SamplingParams(temperature=0.0, max_tokens=30, ignore_eos=True)
+    base = dict(model_config=TARGET, draft_model_config=DRAFT, num_speculative_tokens=4, ngram_min_size=2,
+                ngram_max_size=4, max_num_sequences=4, max_model_length=512, block_size=16, seed=3)
+    out = {}
+    for name, extra in [("spec", {"spec_method": method}), ("spec_eager", {"spec_method": method,
+                                                                           "enforce_eager": True}),
+                        ("plain", {"spec_method": "none"})]:
+        eng = SpecLLMEngine({**base, **extra})
+        res = eng.generate(prompts, sp)
+        out[name] = [o["token_ids"] for o in res["outputs"]]
+        print(name, res["metrics"]["rounds"], res["metrics"]["spec_decoding"], flush=True)
+        if name == "spec" and method == "hybrid":
+            st = res["metrics"]["spec_decoding"]
+            assert st["model_fallback_rounds"] >= 0 and "model_fallback_seqs" in st
+        del eng
+        torch.cuda.empty_cache()
+    assert all(len(x) == 30 for x in out["spec"])
+    assert out["spec"] == out["spec_eager"]
+    assert out["spec"] == out["plain"]
+
+
+@pytest.mark.parametrize("method", ["model", "hybrid"])
+def test_stochastic_round_matches_host_restatement(method):
+    # one eager stochastic round: every draft is the sampler's token on that step's logits and noise,
+    # the acceptance is the reference's on the round's logits, uniforms and noise, then _commit
+    print(f"case: stochastic {method} round vs host restatement", flush=True)
+    K, V = 4, TARGET.vocab_size
+    eng = SpecLLMEngine(dict(model_config=TARGET, draft_model_config=DRAFT, spec_method=method,
+                             num_speculative_tokens=K, ngram_min_size=2, ngram_max_size=4, max_num_sequences=4,
+                             max_model_length=256, block_size=16, enforce_eager=True, seed=9))
+    r = eng._round(True)
+    prompts = prompts_with_spans(8, 4)
+    hists = [prompts[0][:45], prompts[1][:37], [int(x) for x in synth.randint(5, 92, 33, 0, V)], prompts[3][:52]]
+    temps = [1.0, 0.7, 1.0, 0.0]
+    _load(eng, r, hists, temps=temps)
+    B = len(hists)
+    r.body(B)
+    torch.cuda.synchronize()
+    DL = r.draft_logits.float().cpu().numpy()
+    DN = r.draft_noise.cpu().numpy()
+    MD = r.model_drafts[:B].cpu().tolist()
+    for b in range(B):
+        for i in range(K):
+            assert MD[b][i] == oa.sample(DL[i, b], temps[b], DN[i, b]), (b, i)
+    drafts = [r.drafts[b, :int(r.num_drafts[b])].tolist() for b in range(B)]
+    mode = r.draft_mode[:B].cpu().tolist()
+    if method == "hybrid":
+        ng = on.draft(hists, K, 2, 4)
+        for b in range(B):
+            assert drafts[b] == (ng[b] if ng[b] else MD[b]) and mode[b] == int(not ng[b])
+        assert 0 < sum(mode) < B  # the case mixes n-gram and model sequences
+    else:
+        assert drafts == MD and mode == [1] * B
+    T = r.logits[:B * (K + 1)].float().cpu().numpy()
+    U = r.uniforms.cpu().numpy()
+    Q = r.accept_noise.float().cpu().numpy()
+    out = r.out_tokens[:B].cpu().tolist()
+    n = r.out_len[:B].cpu().tolist()
+    for b in range(B):
+        k = len(drafts[b])
+        rows = T[b * (K + 1): b * (K + 1) + k + 1]
+        if mode[b]:
+            noise = Q[b] if method == "model" else Q[b, 0]
+            want = oa.verify(drafts[b], rows, DL[:k, b], temps[b], U[b, :k], noise, "bf16")
+        else:
+            want = oa.verify(drafts[b], rows, None, temps[b], None, Q[b, :k + 1], "bf16")
+        assert out[b][:n[b]] == want, (b, out[b][:n[b]], want)
+        new, _ = orr.commit(hists[b], len(hists[b]) - 2, want, 100, -1, True, None)
+        assert r.history[b, :int(r.hist_len[b])].tolist() == new
+
+
+def test_identical_drafter_is_accepted():
+    # drafter == target (same shape and weights): p_t and p_d agree up to the rounding of two
+    # forward shapes, so min(1, p_t/p_d) is ~1 and nearly every draft is accepted at T = 1
+    print("case: identical drafter", flush=True)
+    K = 4
+    eng = SpecLLMEngine(dict(model_config=TARGET, draft_model_config=TARGET, draft_seed=11, spec_method="model",
+                             num_speculative_tokens=K, max_num_sequences=4, max_model_length=512, block_size=16,
+                             seed=11))
+    res = eng.generate(prompts_with_spans(9, 4), SamplingParams(temperature=1.0, max_tokens=40, ignore_eos=True))
+    st = res["metrics"]["spec_decoding"]
+    print(st, res["metrics"]["rounds"], flush=True)
+    assert all(len(o["token_ids"]) == 40 for o in res["outputs"])
+    # committed tokens per drafted token: (K + 1) / K when everything is accepted
+    assert st["accepted_tokens"] >= 0.9 * st["drafted_tokens"]

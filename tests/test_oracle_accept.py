@@ -169,3 +169,41 @@ def test_stochastic_closed_forms():
     assert len(out) == 1 and out[0] != 7
     # temperature <= 1e-6 dispatches to greedy (rejection_sampler.py:95)
     assert oa.verify([int(np.argmax(x[0])), 0], x[:3], temperature=0.0)[0] == int(np.argmax(x[0]))
+
+
+def sampler_torch(logits, temperature, noise):
+    """layers/sampler.py:14-24's torch calls, executed by torch (an
+    independent path: torch's fp32 softmax and promotion rules)."""
+    greedy = temperature <= 1e-6
+    safe_temperature = torch.where(greedy, torch.ones_like(temperature), temperature)
+    argmax_tokens = logits.argmax(dim=-1)
+    probs = torch.softmax(logits / safe_temperature.unsqueeze(-1), dim=-1)
+    sample_tokens = (probs / noise).argmax(dim=-1)
+    return torch.where(greedy, argmax_tokens, sample_tokens)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_sampler_oracle_reproduces_torch_execution(dtype):
+    # 40 seeds x 6 rows of V = 4096 with mixed temperatures (greedy rows among them)
+    temps = torch.tensor([1.0, 0.0, 0.6, 1.7, 1e-7, 1.0])
+    for seed in range(40):
+        g = torch.Generator().manual_seed(seed)
+        lg = (torch.randn(6, 4096, generator=g) * 2.0).to(TDT[dtype])
+        q = torch.empty(6, 4096).exponential_(1, generator=g).clamp_min_(1e-10)
+        want = sampler_torch(lg, temps, q).tolist()
+        got = oa.sample_rows(lg.float().numpy().astype(np.float64), temps.numpy(), q.numpy())
+        assert got == want, seed
+
+
+def test_sampler_closed_forms():
+    # greedy rows ignore the noise; a one-hot-dominant row samples its peak whatever the noise;
+    # equal logits sample argmin(noise) (p uniform, so argmax(p / q) = argmin q)
+    x = np.zeros(50)
+    x[7] = 80.0
+    q = np.linspace(0.5, 3.0, 50)
+    assert oa.sample(x, 0.0, q) == 7 and oa.sample(x, 1.0, q) == 7
+    flat = np.ones(50)
+    q2 = np.full(50, 2.0)
+    q2[31] = 0.1
+    assert oa.sample(flat, 1.0, q2) == 31
+    assert oa.sample(flat, 0.0, q2) == 0  # argmax ties: first index

@@ -51,3 +51,16 @@ def test_block_manager_speculative_capacity_and_trim():
     assert s.token_ids == [1, 2, 3, 4, 5] and len(s.block_table) == 2
     bm.deallocate(s)
     assert len(bm.free_block_ids) == 6 and not s.block_table
+
+
+def test_draft_rows_layout():
+    # n = 5 tokens, block size 4, table [3, 9]: step 0 feeds positions 3 and 4, steps 1..2 positions 5, 6
+    ids0, pos0, slot0, pos, slots, ctx = orr.draft_rows([[1, 2, 3, 4, 5], [7]], [[3, 9], [2, -1]], 4, 3, [1, 1])
+    assert ids0 == [4, 5, 0, 7] and pos0 == [3, 4, -1, 0]
+    assert slot0 == [3 * 4 + 3, 9 * 4 + 0, -1, 2 * 4 + 0]
+    assert pos == [[4, 0], [5, 1], [6, 2]]
+    assert slots == [[36, 8], [37, 9], [38, 10]]
+    assert ctx == [[5, 1], [6, 2], [7, 3]]    # keys up to the fed position
+    # inactive: pads, context 0
+    ids0, pos0, slot0, pos, slots, ctx = orr.draft_rows([[1, 2, 3]], [[0]], 4, 2, [0])
+    assert (ids0, pos0, slot0) == ([0, 0], [-1, -1], [-1, -1]) and pos == [[-1], [-1]] and ctx == [[0], [0]]
