@@ -172,6 +172,46 @@ def e2e_round(batches=(1, 8), tokens: int = 48, K: int = 8) -> dict:
     return out
 
 
+def e2e_cascade(batches=(1, 8), tokens: int = 48, K: int = 8) -> dict:
+    """a random-init Qwen3-0.6B drafter feeding a
+    random-init Qwen3-8B target (36 layers, hidden 4096, 32Q/8KV, bf16)
+    through the hybrid drafter (n-gram first, K = 8 GPU-resident draft
+    steps otherwise), one 9-row verify forward and min(1, p_t/p_d)
+    acceptance at temperature 1.0; 1200-token prefix, 48 output tokens.
+    Decode tokens per second over the rounds, one hipGraph replay per
+    round."""
+    from naivllm_amd.layers.qwen3 import Qwen3Config
+    from naivllm_amd.sampling_parameters import SamplingParams
+    from naivllm_amd.spec_engine.spec_llm_engine import SpecLLMEngine
+
+    eng = SpecLLMEngine(dict(spec_method="hybrid", num_speculative_tokens=K, ngram_min_size=2, ngram_max_size=4,
+                             model_config=Qwen3Config.qwen3_8b(), draft_model_config=Qwen3Config.qwen3_0_6b(),
+                             max_num_sequences=max(batches), max_model_length=1200 + 16 + tokens + 64,
+                             block_size=256, seed=5))
+    sp = SamplingParams(temperature=1.0, max_tokens=tokens, ignore_eos=True)
+    out = {}
+    for b in batches:
+        before = dict(eng.spec_stats)
+        res = eng.generate(config3_prompts(b, seed=5), sp)
+        m = res["metrics"]
+        st = m["spec_decoding"]
+        out[f"b{b}"] = {
+            "decode_tok_s": round(m["decode_tok_per_s"], 1),
+            "decode_ms_per_round": round(1e3 * m["decode_s"] / max(m["rounds"], 1), 3),
+            "rounds": m["rounds"],
+            "tokens_per_round": round(m["decode_tokens"] / max(m["rounds"], 1), 3),
+            "drafted": st["drafted_tokens"] - before["drafted_tokens"],
+            "accepted": st["accepted_tokens"] - before["accepted_tokens"],
+            "model_fallback_seqs": st["model_fallback_seqs"] - before["model_fallback_seqs"],
+            "prefill_s": round(m["prefill_s"], 3),
+            "output_tokens": m["output_tokens"],
+        }
+        print(f"[bench] cascade b{b}: {out[f'b{b}']}", file=sys.stderr, flush=True)
+    del eng
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(seconds: float) -> dict:
     """The torch-on-CPU restatement of the same verify-attention call
     (config 2 shape, one layer), timed on this host's cores."""
@@ -235,6 +275,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-e2e", action="store_true", help="skip the config-3 end-to-end round measurement")
+    ap.add_argument("--no-cascade", action="store_true",
+                    help="skip the config-5 measurement (Qwen3-0.6B drafter feeding Qwen3-8B, hybrid, T=1)")
     ap.add_argument("--seed", type=int, default=2)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run only a plain device copy of this many MiB (calibrates rocprofv3's "
@@ -283,6 +325,7 @@ def main():
           file=sys.stderr, flush=True)
 
     e2e = None if args.no_e2e else e2e_round()
+    cascade = None if (args.no_e2e or args.no_cascade) else e2e_cascade()
     cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
     line = {
         "metric": METRIC,
@@ -308,6 +351,7 @@ def main():
                      "bytes_per_call": wl.bytes, "mfma_tflops": round(tflops, 2),
                      "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 5)},
         "accepted_tok_s": e2e,
+        "cascade_tok_s": cascade,
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)

@@ -79,8 +79,7 @@ class SpecLLMEngine:
         if self.draft_model is not None:
             self.draft_model.allocate_kv_cache(num_blocks, self.block_size)
         self.eager = config.get("enforce_eager", False) or not config.get("capture_verify", True)
-        self.rounds: dict[bool, VerifyRound] = {}
-        self._round(False)
+        self.rounds: dict[bool, VerifyRound] = {}  # greedy / stochastic round, built on first use
         self.spec_stats = {"method": self.spec_method, "num_speculative_tokens": K, "rounds": 0,
                            "drafted_tokens": 0, "accepted_tokens": 0, "fallback_rounds": 0}
         if self.spec_method == "hybrid":
@@ -88,7 +87,7 @@ class SpecLLMEngine:
 
     @property
     def round(self) -> VerifyRound:
-        """The greedy round (built at construction)."""
+        """The greedy round."""
         return self._round(False)
 
     def _round(self, stochastic: bool) -> VerifyRound:

@@ -198,3 +198,50 @@ def test_identical_drafter_is_accepted():
     assert all(len(o["token_ids"]) == 40 for o in res["outputs"])
     # committed tokens per drafted token: (K + 1) / K when everything is accepted
     assert st["accepted_tokens"] >= 0.9 * st["drafted_tokens"]
+
+
+def test_drop_in_model_and_hybrid_drafters():
+    # the reference's drafter protocol on host Sequences: ModelDrafter.prefill mirrors the prompt,
+    # draft() appends K greedy drafts (== the drafter's own greedy decoding) and returns (K, vocab)
+    # rows; HybridDrafter takes the n-gram continuation where there is one and the model elsewhere
+    print("case: drop-in ModelDrafter / HybridDrafter", flush=True)
+    from naivllm_amd.engine.block_manager import BlockManager
+    from naivllm_amd.layers.qwen3 import Qwen3Verify
+    from naivllm_amd.spec_engine import DraftRunner, HybridDrafter, ModelDrafter, NgramDrafter
+
+    K = 4
+    dm = Qwen3Verify(DRAFT, "cuda", seed=21)
+    runner = DraftRunner(dm, num_blocks=64, block_size=16)
+    bm = BlockManager(64, 16, table_attr="draft_block_table", cached_attr="draft_num_cached_tokens")
+    drafter = ModelDrafter(runner, bm, num_speculative_tokens=K)
+    prompts = [h[:30] for h in prompts_with_spans(12, 2)]
+    seqs = [Sequence(list(p)) for p in prompts]
+    drafter.prefill(seqs)
+    for s in seqs:
+        s.append_token(7)  # the first completion token, after the prefill as in the reference
+    assert drafter.can_draft(seqs, K)
+    tokens, rows = drafter.draft(seqs)
+    assert all(len(t) == K for t in tokens) and all(r.shape == (K, DRAFT.vocab_size) for r in rows)
+    for s, p, t in zip(seqs, prompts, tokens):
+        assert s.token_ids == p + [7] + t and s.draft_tokens == t
+    solo = SpecLLMEngine(dict(model_config=DRAFT, spec_method="none", max_num_sequences=4, max_model_length=256,
+                              block_size=16, enforce_eager=True, seed=21))
+    res = solo.generate([p + [7] for p in prompts], SamplingParams(temperature=0.0, max_tokens=K, ignore_eos=True))
+    assert [o["token_ids"] for o in res["outputs"]] == tokens
+    # each row is the drafter's distribution at that step: its argmax is the greedy draft
+    assert [r.float().argmax(-1).tolist() for r in rows] == tokens
+
+    # hybrid: sequence 0 repeats its spans (n-gram hit), sequence 1 is random (model fallback)
+    seqs = [Sequence(prompts_with_spans(13, 1)[0][:45]), Sequence([int(x) for x in synth.randint(3, 93, 30, 0, 2048)])]
+    drafter.prefill(seqs)
+    for s in seqs:
+        # sequence 0: the token that continues its period-40 span pattern
+        s.append_token(int(s.token_ids[-40]) if len(s.token_ids) >= 40 else 7)
+    hyb = HybridDrafter(NgramDrafter(num_speculative_tokens=K, min_ngram_size=2, max_ngram_size=4), drafter)
+    before = [list(s.token_ids) for s in seqs]
+    lists, rows = hyb.draft(seqs)
+    ng = on.draft(before, K, 2, 4)
+    assert ng[0] and not ng[1]
+    assert lists[0] == ng[0] and rows[0] is None
+    assert len(lists[1]) == K and rows[1] is not None and rows[1].shape == (K, DRAFT.vocab_size)
+    assert hyb.model_rounds == 1 and hyb.model_seqs == 1
