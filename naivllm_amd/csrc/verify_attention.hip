@@ -50,7 +50,17 @@ constexpr int kMaxCounterPairs = 16384;
 // pressure there: on MI355X at config 2, 2 stages take 20.6 us, 3 21.3 us,
 // 4 23.2 us.  So 2, the floor of the register estimate used for the
 // key-split kernel below.
-constexpr int bf16_stages(int, int, int, bool) { return 2; }
+#ifndef NSV_DSLICE_STAGES
+#define NSV_DSLICE_STAGES 2
+#endif
+constexpr int bf16_stages(int MT, int DH, int DC, bool UPAGE) {
+  // register estimate of a deeper pipeline (tiles of 40 VGPRs beyond a fixed part), floored at 2
+  const int KS = DH / 32, DT = DC / 16, VL = 32 * (DC / 8) / 64;
+  const int fixed = 20 + MT * (KS * 4 + DT * 4 + 12) + (UPAGE ? 32 : 64);
+  const int fit = (256 - fixed) / (8 * KS + 4 * VL);
+  const int want = NSV_DSLICE_STAGES;
+  return want < 2 ? 2 : (want > fit ? (fit < 2 ? 2 : fit) : want);
+}
 constexpr float kNegInf = -__builtin_inff();
 
 struct VerifyArgs {
@@ -181,7 +191,17 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
   constexpr int VSTR = DC + 16;  // staged V row stride (bf16): an odd multiple of 32 bytes,
                                  // so the transposing reads of 8 rows hit distinct banks
   constexpr int RSTR = DC + 4;   // merge-region row stride (floats)
-  constexpr int STAGE = NW * kTile * VSTR * 2;
+  // UPAGE: K tiles are loaded as whole 2*DH-byte rows (CPR 16-byte chunks
+  // per key, KPI keys per load) and reshaped through a per-wave LDS tile
+  // into the MFMA operand layout, with chunk X of key r stored at slot
+  // X ^ (r % CPR): the row-order writes and the operand-order reads then hit
+  // distinct LDS banks.  (A CU ingests whole-row loads several times faster
+  // than the operand order's 64 bytes from each of 16 keys 2 KB apart.)
+  constexpr int CPR = DH / 8;
+  constexpr int KPI = NSV_WAVE / CPR;
+  constexpr int KROW = DH * 2;
+  constexpr int KSTAGE = UPAGE ? NW * kTile * KROW : 0;
+  constexpr int STAGE = NW * kTile * VSTR * 2 + KSTAGE;
   constexpr int MTILE_BYTES = NW * 16 * RSTR * 4;  // one m-tile of every wave's O
   constexpr int MTP0 = (72 * 1024) / MTILE_BYTES;
   constexpr int MTP = MTP0 < 1 ? 1 : (MTP0 > MT ? MT : MTP0);  // m-tiles merged per pass
@@ -286,13 +306,15 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
   const bf16_t* kbase = (const bf16_t*)a.k_cache + hk * DH;
   const bf16_t* vbase = (const bf16_t*)a.v_cache + hk * DH + dq * DC;
   uint16_t* vl = reinterpret_cast<uint16_t*>(smem) + w * kTile * VSTR;
+  unsigned char* kl = smem + NW * kTile * VSTR * 2 + (UPAGE ? w * kTile * KROW : 0);
   __syncthreads();  // block-table slice visible
 
   const int ntiles = (tok_end - tok_begin + kTile - 1) / kTile;
   const int niter = (ntiles + NW - 1) / NW;  // same trip count in every wave
 
   struct Tile {
-    u32x4 k[2][KS];  // K as the A operand: lane (g4, c) holds key 16*t + c, dims 32*ks + 8*g4 .. +7
+    u32x4 k[2][KS];  // UPAGE: whole rows, load j = t*KS + ks, lane -> (key KPI*j + lane/CPR, chunk lane%CPR);
+                     // else the A operand: lane (g4, c) holds key 16*t + c, dims 32*ks + 8*g4 .. +7
     u32x4 v[VL];     // V slice rows, coalesced: chunk j*64 + lane = (key, 16-byte chunk)
     uint64_t kmask;  // keys of the tile that exist (inside the split, page mapped)
     int n0;
@@ -320,12 +342,13 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
       const unsigned base_key = (unsigned)(T.n0 & bs_mask);
       const unsigned row_bytes = (unsigned)tok_stride * 2;
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const int r = t * 16 + c;
-        const unsigned off = (base_key + (r < nvalid ? r : 0)) * row_bytes + g4 * 16;
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int ks = 0; ks < KS; ++ks) T.k[t][ks] = load16(kp + off + ks * 64);
-      }
+        for (int ks = 0; ks < KS; ++ks) {
+          const int r = KPI * (t * KS + ks) + lane / CPR;
+          const unsigned off = (base_key + (r < nvalid ? r : 0)) * row_bytes + (lane % CPR) * 16;
+          T.k[t][ks] = load16(kp + off);
+        }
 #pragma unroll
       for (int j = 0; j < VL; ++j) {
         const int id = j * NSV_WAVE + lane;
@@ -365,6 +388,30 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
 
   auto compute = [&](const Tile& T) {
     if (T.kmask == 0) return;  // uniform: nothing of this tile exists
+    // K operands: UPAGE reshapes the row-order tile through LDS (this wave's
+    // rows; a wave's LDS ops complete in order)
+    u32x4 kA[2][KS];
+    if constexpr (UPAGE) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const int r = KPI * (t * KS + ks) + lane / CPR;
+          *reinterpret_cast<u32x4*>(kl + r * KROW + (((lane % CPR) ^ (r % CPR)) << 4)) = T.k[t][ks];
+        }
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+          const int r = t * 16 + c;
+          kA[t][ks] = *reinterpret_cast<const u32x4*>(kl + r * KROW + (((ks * 4 + g4) ^ (r % CPR)) << 4));
+        }
+    } else {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) kA[t][ks] = T.k[t][ks];
+    }
     // S^T tile: lane (g4, c), element i -> key 16*t + 4*g4 + i, query row 16*mt + c.
     f32x4 sacc[2][MT];
 #pragma unroll
@@ -374,7 +421,7 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
         f32x4 sv = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
-          sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(T.k[t][ks]), qB[mt][ks], sv, 0, 0, 0);
+          sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kA[t][ks]), qB[mt][ks], sv, 0, 0, 0);
         sacc[t][mt] = sv;
       }
     // Stage the V slice (this wave's private LDS rows; LDS ops of one wave
