@@ -264,6 +264,30 @@ int nsv_qk_norm_rope_store(const void* qkv, const void* q_norm_w,
                            int Hkv, int D, float eps, void* stream);
 int nsv_silu_mul(const void* gate_up, void* out, int T, int I, void* stream);
 
+/*
+ * Few-row bf16 linear layer of the verify forward: y = h W^T for the
+ * M = B*(K+1) verify rows, W [N, K] row-major, fp32 accumulation, one bf16
+ * rounding per output.  Replaces the F.linear projections of
+ * src/myvllm/layers/linear.py (qkv_proj, o_proj, gate_up_proj, down_proj,
+ * models/qwen3.py:74-151) and the LM head (layers/embedding_head.py:71-95),
+ * and fuses their neighbours:
+ *   norm_w != NULL: h = rmsnorm(x) * norm_w (layers/layernorm.py:18-35)
+ *     with x the bf16 residual stream [M, K] and ss_in [nss_in, M] the
+ *     partial sums of x^2 per row that a residual epilogue wrote (summed in
+ *     a fixed order); otherwise h = x.
+ *   epilogue 0: y [M, N] = h W^T.
+ *   epilogue 1 (SiluAndMul, layers/activation.py:17-19): W holds
+ *     [gate; up] ([N = 2I, K]); y [M, I] = silu(gate) * up.
+ *   epilogue 2 (the residual add of layernorm.py:29-31): resid [M, N] =
+ *     bf16(h W^T) + resid, and ss_out [N/16, M] receives the partial sums
+ *     of the new resid^2 over each 16-column tile; y is unused.
+ * N % 16 == 0, K % 8 == 0.
+ */
+int nsv_linear(const void* x, const void* norm_w, const float* ss_in,
+               int nss_in, float eps, const void* weight, void* y,
+               void* resid, float* ss_out, int M, int N, int K,
+               int epilogue, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -5,12 +5,16 @@ Qwen3Attention :11-123, Qwen3MLP :129-151, Qwen3DecoderLayer :159-227,
 Qwen3Model :233-281, Qwen3ForCausalLM :287-344): embedding, N decoder
 layers (RMSNorm, fused QKV projection, per-head q/k RMSNorm, NeoX RoPE,
 paged KV store + paged verify attention, o_proj, RMSNorm with residual,
-SwiGLU MLP), final norm, LM head over every row.  The four GEMMs per layer
-and the LM head are PyTorch-ROCm (hipBLASLt); everything between them is
-this library's gfx950 kernels: residual add + RMSNorm, the pre-attention
-epilogue (q/k RMSNorm + RoPE + paged KV store), verify attention and
-SiLU * up -- 4 GEMMs + 4 kernels per layer.  Weights are random (seeded):
-no checkpoint is loaded.
+SwiGLU MLP), final norm, LM head over every row.  Up to FUSED_ROWS verify
+rows every layer runs on this library's gfx950 kernels, 6 launches per
+layer: the QKV projection (with the input RMSNorm as its prologue), the
+pre-attention epilogue (q/k RMSNorm + RoPE + paged KV store), verify
+attention, o_proj (with the residual add as its epilogue), gate_up
+(post-attention RMSNorm prologue, SiLU * up epilogue) and down (residual
+add epilogue).  Wider batches run the projections on hipBLASLt between
+this library's residual-RMSNorm, epilogue, attention and SiLU kernels; the
+LM head is hipBLASLt in both.  Weights are random (seeded): no checkpoint
+is loaded.
 
 The forward takes the verify metadata explicitly (positions, slots, block
 tables, context lengths, cu_seqlens) so a whole forward is capturable in a
@@ -85,10 +89,37 @@ def qk_norm_rope_store(qkv, q_norm_w, k_norm_w, cos_sin, positions, slot_mapping
     _lib.check(rc, "qk_norm_rope_store")
 
 
+def linear(x: torch.Tensor, weight: torch.Tensor, y: torch.Tensor | None = None, *,
+           norm_w: torch.Tensor | None = None, ss_in: torch.Tensor | None = None, eps: float = 1e-6,
+           swiglu: bool = False, resid: torch.Tensor | None = None, ss_out: torch.Tensor | None = None) -> None:
+    """y = h @ weight.T on this library's few-row kernel (nsv_linear).
+
+    h = rmsnorm(x) * norm_w when norm_w is given (x is then the residual
+    stream and ss_in [n, M] the producer's partial sums of x^2), else x.
+    swiglu: weight is [gate; up] and y = silu(gate) * up.  resid: instead of
+    writing y, add the product into the residual stream resid [M, N] and
+    write the new partial sums of resid^2 to ss_out [N / 16, M]."""
+    M, K = x.shape
+    N = weight.shape[0]
+    epi = 2 if resid is not None else (1 if swiglu else 0)
+    nss = ss_in.shape[0] if ss_in is not None else 0
+    rc = _lib.lib().nsv_linear(x.data_ptr(), _lib.ptr(norm_w), _lib.ptr(ss_in), nss, eps, weight.data_ptr(),
+                               _lib.ptr(y), _lib.ptr(resid), _lib.ptr(ss_out), M, N, K, epi,
+                               _lib.stream_ptr(x.device))
+    _lib.check(rc, "linear")
+
+
 def silu_mul(gate_up: torch.Tensor, out: torch.Tensor) -> None:
     rc = _lib.lib().nsv_silu_mul(gate_up.data_ptr(), out.data_ptr(), gate_up.shape[0], out.shape[1],
                                  _lib.stream_ptr(gate_up.device))
     _lib.check(rc, "silu_mul")
+
+
+# Verify rows up to which the forward runs on the fused few-row linear
+# kernel; beyond it hipBLASLt's tiles reuse the activations better (measured
+# on MI355X: at 9-18 rows the fused kernel is ahead per projection, at 72
+# rows hipBLASLt is up to 2x faster).
+FUSED_ROWS = 48
 
 
 class Qwen3Verify:
@@ -148,27 +179,51 @@ class Qwen3Verify:
         eps = cfg.rms_norm_eps
         T = input_ids.shape[0]
         block_m = max(16, 1 << (max_q_len - 1).bit_length())
+        I = cfg.intermediate_size
         x = F.embedding(input_ids, self.embed)
-        residual = torch.empty_like(x)
+        resid = torch.empty_like(x)  # the residual stream
         h = torch.empty_like(x)
         q = torch.empty(T, H, D, dtype=self.dtype, device=self.device)
-        act = torch.empty(T, cfg.intermediate_size, dtype=self.dtype, device=self.device)
-        for li, L in enumerate(self.layers):
-            if li == 0:
-                rms_norm(x, L["ln1"], eps, h, residual_out=residual)
-            else:
-                rms_norm(x, L["ln1"], eps, h, residual=residual, residual_out=residual)
-            qkv = F.linear(h, L["qkv"])
-            qk_norm_rope_store(qkv, L["q_norm"], L["k_norm"], self.rope, positions, slot_mapping, q,
-                               self.k_caches[li], self.v_caches[li], H, Hkv, D, eps)
-            o = paged_attention_verify(q, self.k_caches[li], self.v_caches[li], block_tables, context_lens,
-                                       cu_seqlens_q, positions, self.scale, H, Hkv, D, self.block_size, block_m,
-                                       max_q_len=max_q_len)
-            x = F.linear(o.view(T, H * D), L["o"])
-            rms_norm(x, L["ln2"], eps, h, residual=residual, residual_out=residual)
-            silu_mul(F.linear(h, L["gate_up"]), act)
-            x = F.linear(act, L["down"])
-        rms_norm(x, self.norm, eps, h, residual=residual)
+        attn = lambda li: paged_attention_verify(  # noqa: E731
+            q, self.k_caches[li], self.v_caches[li], block_tables, context_lens, cu_seqlens_q, positions,
+            self.scale, H, Hkv, D, self.block_size, block_m, max_q_len=max_q_len)
+        rms_norm(x, self.layers[0]["ln1"], eps, h, residual_out=resid)
+        if T <= FUSED_ROWS:
+            # Every RMSNorm after layer 0's is the prologue of the projection
+            # that consumes it and every residual add the epilogue of the
+            # projection that produces it: 6 launches per layer.
+            qkv = torch.empty(T, (H + 2 * Hkv) * D, dtype=self.dtype, device=self.device)
+            act = torch.empty(T, I, dtype=self.dtype, device=self.device)
+            ss_o = torch.empty(E // 16, T, dtype=torch.float32, device=self.device)  # partial sums of resid^2
+            ss_d = torch.empty(E // 16, T, dtype=torch.float32, device=self.device)
+            for li, L in enumerate(self.layers):
+                if li == 0:
+                    linear(h, L["qkv"], qkv)
+                else:
+                    linear(resid, L["qkv"], qkv, norm_w=L["ln1"], ss_in=ss_d, eps=eps)
+                qk_norm_rope_store(qkv, L["q_norm"], L["k_norm"], self.rope, positions, slot_mapping, q,
+                                   self.k_caches[li], self.v_caches[li], H, Hkv, D, eps)
+                linear(attn(li).view(T, H * D), L["o"], resid=resid, ss_out=ss_o)
+                linear(resid, L["gate_up"], act, norm_w=L["ln2"], ss_in=ss_o, eps=eps, swiglu=True)
+                linear(act, L["down"], resid=resid, ss_out=ss_d)
+            rms_norm(resid, self.norm, eps, h)
+        else:
+            # wider batches: hipBLASLt projections between this library's
+            # norm / epilogue / SiLU kernels (9 launches per layer)
+            act = torch.empty(T, I, dtype=self.dtype, device=self.device)
+            for li, L in enumerate(self.layers):
+                if li > 0:
+                    rms_norm(x, L["ln1"], eps, h, residual=resid, residual_out=resid)
+                qkv = F.linear(h, L["qkv"])
+                qk_norm_rope_store(qkv, L["q_norm"], L["k_norm"], self.rope, positions, slot_mapping, q,
+                                   self.k_caches[li], self.v_caches[li], H, Hkv, D, eps)
+                x = F.linear(attn(li).view(T, H * D), L["o"])
+                rms_norm(x, L["ln2"], eps, h, residual=resid, residual_out=resid)
+                silu_mul(F.linear(h, L["gate_up"]), act)
+                x = F.linear(act, L["down"])
+            rms_norm(x, self.norm, eps, h, residual=resid)
+        # the LM head stays on hipBLASLt: over 152k columns its large tiles
+        # stream the 311 MB weight faster than the few-row kernel
         if logits_out is None:
             return F.linear(h, self.lm_head)
         torch.matmul(h, self.lm_head.t(), out=logits_out)

@@ -127,3 +127,15 @@ def test_accept_and_ngram_reject_bad_arguments_before_launch():
     assert h.nsv_ngram_draft(1, 1, 10, 2, 2, 65, 8, 1, 1, None) == -1
     assert h.nsv_ngram_draft(1, 1, 10, 2, 2, 4, 0, 1, 1, None) == -1
     assert h.nsv_ngram_draft(1, 1, 10, 0, 2, 4, 8, 1, 1, None) == 0
+
+
+def test_linear_rejects_bad_arguments_before_launch():
+    h = _lib.lib()
+    # x, norm_w, ss_in, nss_in, eps, weight, y, resid, ss_out, M, N, K, epilogue, stream
+    assert h.nsv_linear(1, None, None, 0, 1e-6, 1, 1, None, None, 9, 1000, 1024, 0, None) == -2  # N % 16
+    assert h.nsv_linear(1, None, None, 0, 1e-6, 1, 1, None, None, 9, 1024, 1020, 0, None) == -2  # K % 8
+    assert h.nsv_linear(None, None, None, 0, 1e-6, 1, 1, None, None, 9, 1024, 1024, 0, None) == -1
+    assert h.nsv_linear(1, None, None, 0, 1e-6, 1, 1, None, None, 9, 1024, 1024, 3, None) == -1
+    assert h.nsv_linear(1, 1, None, 0, 1e-6, 1, 1, None, None, 9, 1024, 1024, 0, None) == -1  # norm without sums
+    assert h.nsv_linear(1, None, None, 0, 1e-6, 1, None, None, None, 9, 1024, 1024, 2, None) == -1  # no stream
+    assert h.nsv_linear(1, None, None, 0, 1e-6, 1, 1, None, None, 0, 1024, 1024, 0, None) == 0  # no rows

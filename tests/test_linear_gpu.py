@@ -1,0 +1,134 @@
+"""The few-row linear kernel (nsv_linear) against plain PyTorch fp32
+restatements of the ops it replaces or fuses: F.linear (layers/linear.py),
+residual RMSNorm (layers/layernorm.py:18-35) as its prologue, SiluAndMul
+(layers/activation.py:17-19) and the residual add as its epilogues.
+
+Tolerances: every output is one bf16 rounding of an fp32 result, held to
+the bf16 contract (2e-2 abs / 1e-2 rel) with operands scaled so outputs are
+O(1).  The normalised activation is rounded to bf16 before the product, as
+the reference's RMSNorm output is a bf16 tensor, and the restatement does
+the same.  The residual stream is checked against bf16(bf16(x W^T) + r) and
+the partial sums of squares against the fp32 sums of the returned stream
+over each 16-column tile."""
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from naivllm_amd.layers import qwen3 as qm
+
+pytestmark = pytest.mark.gpu
+
+BF16 = dict(atol=2e-2, rtol=1e-2)
+
+# (M, N, K): Qwen3-0.6B projections at b1 / b2 / b8, an 8B projection, more
+# rows than one workgroup row-chunk (80), a reduction that is not a
+# multiple of the 1024-element wave round, and the test model's shapes
+SHAPES = [(9, 4096, 1024), (18, 1024, 2048), (72, 6144, 1024), (72, 1024, 3072), (16, 6144, 4096),
+          (100, 512, 1024), (1, 256, 256), (37, 2048, 264)]
+
+
+def gen(seed):
+    g = torch.Generator(device="cuda")
+    g.manual_seed(seed)
+    return g
+
+
+def randn(g, *shape, scale=1.0):
+    return (torch.randn(*shape, generator=g, device="cuda") * scale).to(torch.bfloat16)
+
+
+def partial_squares(r: torch.Tensor, tiles: int) -> torch.Tensor:
+    """[tiles, M] fp32 partial sums of r^2, as a residual epilogue writes them."""
+    M, K = r.shape
+    return r.float().pow(2).view(M, tiles, K // tiles).sum(-1).t().contiguous()
+
+
+def norm_ref(r: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    rf = r.float()
+    return (rf / torch.sqrt(rf.pow(2).mean(-1, keepdim=True) + eps) * w.float()).to(torch.bfloat16).float()
+
+
+@pytest.mark.parametrize("M,N,K", SHAPES)
+@pytest.mark.parametrize("norm", [False, True])
+def test_linear_plain(M, N, K, norm):
+    print(f"case: linear plain M={M} N={N} K={K} norm={norm}", flush=True)
+    g = gen(M * 31 + N + K)
+    x = randn(g, M, K)
+    w = randn(g, N, K, scale=K ** -0.5)
+    y = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    if norm:
+        nw = (1.0 + 0.3 * torch.randn(K, generator=g, device="cuda")).to(torch.bfloat16)
+        tiles = 8 if K % 8 == 0 else 1
+        qm.linear(x, w, y, norm_w=nw, ss_in=partial_squares(x, tiles), eps=1e-6)
+        h = norm_ref(x, nw, 1e-6)
+    else:
+        qm.linear(x, w, y)
+        h = x.float()
+    torch.testing.assert_close(y.float(), h @ w.float().t(), **BF16)
+
+
+@pytest.mark.parametrize("M,I,K", [(9, 3072, 1024), (72, 3072, 1024), (5, 128, 256), (90, 256, 512)])
+def test_linear_swiglu(M, I, K):
+    print(f"case: linear swiglu M={M} I={I} K={K}", flush=True)
+    g = gen(M + I + K)
+    r = randn(g, M, K)
+    w = randn(g, 2 * I, K, scale=K ** -0.5)
+    nw = (1.0 + 0.3 * torch.randn(K, generator=g, device="cuda")).to(torch.bfloat16)
+    y = torch.empty(M, I, dtype=torch.bfloat16, device="cuda")
+    qm.linear(r, w, y, norm_w=nw, ss_in=partial_squares(r, 4), eps=1e-6, swiglu=True)
+    gu = (norm_ref(r, nw, 1e-6) @ w.float().t()).to(torch.bfloat16).float()  # the bf16 gate_up tensor
+    want = F.silu(gu[:, :I]) * gu[:, I:]
+    torch.testing.assert_close(y.float(), want, **BF16)
+
+
+@pytest.mark.parametrize("M,N,K", [(9, 1024, 2048), (72, 1024, 3072), (100, 256, 512), (3, 4096, 4096)])
+def test_linear_residual(M, N, K):
+    print(f"case: linear residual M={M} N={N} K={K}", flush=True)
+    g = gen(M * 7 + N * 3 + K)
+    x = randn(g, M, K)
+    w = randn(g, N, K, scale=K ** -0.5)
+    r0 = randn(g, M, N)
+    r = r0.clone()
+    ss = torch.full((N // 16, M), float("nan"), device="cuda")
+    qm.linear(x, w, resid=r, ss_out=ss)
+    prod = (x.float() @ w.float().t()).to(torch.bfloat16)
+    torch.testing.assert_close(r.float(), (prod.float() + r0.float()).to(torch.bfloat16).float(), **BF16)
+    torch.testing.assert_close(ss, partial_squares(r, N // 16), rtol=1e-5, atol=1e-5)
+
+
+def test_linear_chain_matches_unfused_layer():
+    # o_proj (residual epilogue) -> gate_up (RMSNorm prologue, SwiGLU) ->
+    # down (residual epilogue) -> LM head (RMSNorm prologue): the fused
+    # chain of one decoder layer against the unfused bf16 sequence
+    print("case: linear chain vs unfused layer", flush=True)
+    g = gen(5)
+    M, E, I, V = 18, 1024, 3072, 4096
+    o = randn(g, M, 2048)
+    resid = randn(g, M, E)
+    w_o = randn(g, E, 2048, scale=2048 ** -0.5)
+    w_gu = randn(g, 2 * I, E, scale=E ** -0.5)
+    w_d = randn(g, E, I, scale=I ** -0.5)
+    w_lm = randn(g, V, E, scale=E ** -0.5)
+    ln2 = (1.0 + 0.3 * torch.randn(E, generator=g, device="cuda")).to(torch.bfloat16)
+    ln_f = (1.0 + 0.3 * torch.randn(E, generator=g, device="cuda")).to(torch.bfloat16)
+
+    r = resid.clone()
+    ss_o = torch.empty(E // 16, M, device="cuda")
+    ss_d = torch.empty(E // 16, M, device="cuda")
+    act = torch.empty(M, I, dtype=torch.bfloat16, device="cuda")
+    logits = torch.empty(M, V, dtype=torch.bfloat16, device="cuda")
+    qm.linear(o, w_o, resid=r, ss_out=ss_o)
+    qm.linear(r, w_gu, act, norm_w=ln2, ss_in=ss_o, swiglu=True)
+    qm.linear(act, w_d, resid=r, ss_out=ss_d)
+    qm.linear(r, w_lm, logits, norm_w=ln_f, ss_in=ss_d)
+
+    bf = lambda t: t.to(torch.bfloat16).float()  # noqa: E731
+    x = bf(o.float() @ w_o.float().t())
+    rr = bf(x + resid.float())
+    gu = bf(norm_ref(rr.to(torch.bfloat16), ln2, 1e-6) @ w_gu.float().t())
+    a = bf(F.silu(gu[:, :I]) * gu[:, I:])
+    rr = bf(bf(a @ w_d.float().t()) + rr)
+    want = norm_ref(rr.to(torch.bfloat16), ln_f, 1e-6) @ w_lm.float().t()
+    rel = (logits.float() - want).norm() / want.norm()
+    assert rel < 1e-2, float(rel)
