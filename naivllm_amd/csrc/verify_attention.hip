@@ -215,6 +215,13 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
   __shared__ float row_l[MP];
   __shared__ float row_ms[MP];
   __shared__ int row_pos[MP];
+  // PARK: each wave parks its unscaled O slice and (max, sum) in LDS of its
+  // own as soon as its tiles are done, while slower waves still stream; one
+  // barrier later every output is the factor-weighted sum of the parked
+  // slices.  Taken when the parking area fits beside the staging area.
+  constexpr int PARK_FLOATS = NW * MP * RSTR;
+  constexpr bool PARK = SMEM + PARK_FLOATS * 4 + kMaxSplitPages * 4 + 2 * NW * MP * 4 + 3 * MP * 4 <= 159 * 1024;
+  __shared__ __attribute__((aligned(16))) float park[PARK ? PARK_FLOATS : 4];
 
   // ---- workgroup -> (pair, dq, split); every workgroup of a pair on one XCD
   const int wg = blockIdx.x;
@@ -529,6 +536,56 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
       red_l[w][mt * 16 + c] = l_run[mt];
     }
   }
+  const int64_t pbase = ((int64_t)pair * a.S + split) * a.Mv;
+  if constexpr (PARK) {
+    // lane (g4, c) element i of tile (dt, mt) is O[16*mt + c][16*dt + 4*g4 + i]
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int dt = 0; dt < DT; ++dt)
+        *reinterpret_cast<f32x4*>(&park[(w * MP + mt * 16 + c) * RSTR + dt * 16 + g4 * 4]) = acc[dt][mt];
+    __syncthreads();
+    constexpr int C4 = DC / 4;
+    for (int qd = tid; qd < a.Mv * C4; qd += NT) {
+      const int m = qd / C4, c4 = qd - m * C4;
+      float M = kNegInf;
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, red_m[ww][m]);
+      const float ref = (M == kNegInf) ? 0.f : M;
+      f32x4 o = {0.f, 0.f, 0.f, 0.f};
+      float L = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww) {
+        const float f = __builtin_amdgcn_exp2f((red_m[ww][m] - ref) * sc);
+        L = fmaf(red_l[ww][m], f, L);
+        o += f * *reinterpret_cast<const f32x4*>(&park[(ww * MP + m) * RSTR + c4 * 4]);
+      }
+      if (nsplit == 1) {
+        const int g = m / a.QL, t = m - g * a.QL;
+        if (t >= qlen) continue;
+        const float inv = (L > 0.f && row_pos[m] >= 0) ? 1.f / L : 0.f;
+        bf16_t* dst = (bf16_t*)a.out + ((int64_t)(q0 + t) * a.H + hk * a.G + g) * DH + dq * DC + c4 * 4;
+        const uint32_t lo = (uint32_t)f32_to_bf16_bits(o[0] * inv) | ((uint32_t)f32_to_bf16_bits(o[1] * inv) << 16);
+        const uint32_t hi = (uint32_t)f32_to_bf16_bits(o[2] * inv) | ((uint32_t)f32_to_bf16_bits(o[3] * inv) << 16);
+        *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+      } else {
+        if (row_pos[m] < 0) o = f32x4{0.f, 0.f, 0.f, 0.f};
+        *reinterpret_cast<f32x4*>(&a.part_o[(pbase + m) * DH + dq * DC + c4 * 4]) = o;
+      }
+    }
+    if (nsplit > 1 && dq == 0 && tid < a.Mv) {
+      float M = kNegInf;
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, red_m[ww][tid]);
+      const float ref = (M == kNegInf) ? 0.f : M;
+      float L = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww) L += red_l[ww][tid] * __builtin_amdgcn_exp2f((red_m[ww][tid] - ref) * sc);
+      a.part_ml[(pbase + tid) * 2 + 0] = row_pos[tid] >= 0 && M != kNegInf ? M * sc : kNegInf;
+      a.part_ml[(pbase + tid) * 2 + 1] = row_pos[tid] >= 0 ? L : 0.f;
+    }
+    return;
+  }
   __syncthreads();  // also: every wave is done with its V staging rows
   if (tid < MP) {
     float M = kNegInf;
@@ -552,7 +609,6 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
   }
   float* region = reinterpret_cast<float*>(smem);  // [NW][MTP * 16][RSTR]
   constexpr int C4 = DC / 4;
-  const int64_t pbase = ((int64_t)pair * a.S + split) * a.Mv;
 #pragma unroll
   for (int mp = 0; mp < MT; mp += MTP) {
     if (mp > 0) __syncthreads();  // previous pass fully read
