@@ -274,7 +274,9 @@ int nsv_silu_mul(const void* gate_up, void* out, int T, int I, void* stream);
  *   norm_w != NULL: h = rmsnorm(x) * norm_w (layers/layernorm.py:18-35)
  *     with x the bf16 residual stream [M, K] and ss_in [nss_in, M] the
  *     partial sums of x^2 per row that a residual epilogue wrote (summed in
- *     a fixed order); otherwise h = x.
+ *     a fixed order), evaluated as y = inv_rms(x) * (x W'^T) with
+ *     W' = bf16(W * norm_w) (the norm weight folded into the weight rows);
+ *     otherwise h = x.
  *   epilogue 0: y [M, N] = h W^T.
  *   epilogue 1 (SiluAndMul, layers/activation.py:17-19): W holds
  *     [gate; up] ([N = 2I, K]); y [M, I] = silu(gate) * up.

@@ -4,21 +4,23 @@
 // The verify forward multiplies B*(K+1) activation rows (72 at batch 8) by weight
 // matrices of 2-300 MB, so streaming the weights, not arithmetic, bounds
 // every projection.  A workgroup owns 16 output columns (16 weight rows):
-// its 8 waves take 128-element chunks of the reduction dimension in turn,
+// its 8 waves take 64- or 128-element chunks of the reduction dimension in
+// turn,
 // load their slice of the 16
-// rows as whole-row 16-byte loads (16 lanes cover 256 contiguous bytes of
-// one row), reshape it through a per-wave LDS tile into the MFMA operand
-// layout and multiply it with every activation row
+// rows and of every activation row as whole-row 16-byte loads (8 or 16
+// lanes cover one row's contiguous chunk), reshape both through a per-wave
+// LDS tile into the MFMA operand layout and multiply them
 // (v_mfma_f32_16x16x32_bf16, rows padded to 16; more than 80 rows take
 // further workgroup rows of the grid); the waves' partial
 // products are summed through LDS.  The next chunk's loads are issued
 // before the current chunk is multiplied.
 //
 // Fused stages (each removes a kernel launch and an activation round trip):
-//   * prologue RMSNorm (norm_w != NULL): the activation row is
-//     rmsnorm(r) * norm_w with r the bf16 residual stream; sum(r^2) per row
-//     arrives as per-tile partial sums from the producing linear and is
-//     added in a fixed order;
+//   * prologue RMSNorm (norm_w != NULL): the activation is rmsnorm(r) *
+//     norm_w with r the bf16 residual stream, computed as
+//     inv(r) * (r W'^T), W' = bf16(W * norm_w) formed as the weight rows are
+//     staged; sum(r^2) per row arrives as per-tile partial sums from the
+//     producing linear and is added in a fixed order;
 //   * epilogue SwiGLU: the weight is [gate; up] ([2I, K]); a tile takes 8
 //     gate rows and the matching 8 up rows and writes silu(gate) * up;
 //   * epilogue residual: r = bf16(x) + r (x the product) rewrites the
@@ -35,8 +37,6 @@ namespace {
 constexpr int kLinWaves = 8;
 constexpr int kLinThreads = kLinWaves * 64;
 constexpr int kBN = 16;            // output columns per workgroup
-constexpr int kKC = 128;           // reduction elements per wave chunk
-constexpr int kWStr = kKC + 8;     // staged weight row stride (bf16): 272 bytes, distinct banks per row
 constexpr int kMaxRows = 80;       // activation rows (5 MFMA row tiles)
 
 struct LinearArgs {
@@ -53,14 +53,26 @@ struct LinearArgs {
 };
 
 __device__ __forceinline__ bf16x8 to_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+// two floats to packed bf16, round to nearest even (gfx950's v_cvt_pk_bf16_f32)
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2v){lo, hi}, bf16x2v));
+}
 __device__ __forceinline__ float bfv(uint32_t word, int hi) { return __uint_as_float(hi ? (word & 0xffff0000u) : (word << 16)); }
 
 template <int MT, bool NORM, int EPI>  // EPI 0: plain, 1: SwiGLU, 2: residual
 __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinearArgs a) {
   constexpr int MP = MT * 16;
-  constexpr int WST = kLinWaves * kBN * kWStr * 2;       // staged weight chunks, bytes
-  constexpr int RED = kLinWaves * MP * (kBN + 1) * 4;    // cross-wave partial products, bytes
-  constexpr int SMEM = WST > RED ? WST : RED;
+  constexpr int KC = MT <= 2 ? 128 : 64;  // reduction elements per wave chunk (LDS holds 8 waves' chunks)
+  constexpr int LPR = KC / 8;             // lanes per row of a whole-row load (16 bytes each)
+  constexpr int RPI = 64 / LPR;           // rows per load instruction
+  constexpr int STR = KC + 8;             // staged row stride (bf16): 16-byte reads of 16 rows hit distinct banks
+  constexpr int WL = kBN / RPI;           // weight loads per lane and chunk
+  constexpr int AL = MP / RPI;            // activation loads per lane and chunk
+  constexpr int STAGE = kLinWaves * (kBN + MP) * STR * 2;  // staged chunks, bytes
+  constexpr int RED = kLinWaves * MP * (kBN + 1) * 4;      // cross-wave partial products, bytes
+  constexpr int SMEM = STAGE > RED ? STAGE : RED;
   __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM];
   __shared__ float inv_s[MP];
   __shared__ float ss_s[kLinThreads];
@@ -69,92 +81,80 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinearArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g4 = lane >> 4, c = lane & 15;
+  const int rr = lane / LPR, cc = lane % LPR;  // whole-row load: row rr + RPI j, elements 8 cc .. 8 cc + 7
   const int K = a.K;
   // rows of this workgroup: chunk blockIdx.y of kMaxRows rows
   const int row0 = blockIdx.y * kMaxRows;
   const int M = min(a.M - row0, kMaxRows);
 
-  // weight row of tile column cc
+  // weight row of tile column col
   const int half = a.N >> 1;
-  auto wrow = [&](int cc) -> int64_t {
-    if constexpr (EPI == 1) return cc < 8 ? tile * 8 + cc : half + tile * 8 + (cc - 8);
-    else return (int64_t)tile * kBN + cc;
+  auto wrow = [&](int col) -> int64_t {
+    if constexpr (EPI == 1) return col < 8 ? tile * 8 + col : half + tile * 8 + (col - 8);
+    else return (int64_t)tile * kBN + col;
   };
-  // the reduction in chunks of kKC elements, dealt to the waves round-robin
+  // the reduction in chunks of KC elements, dealt to the waves round-robin
   // (chunk w + 8i is wave w's i-th); a last partial chunk reads zeros past K
-  const int nck = (K + kKC - 1) / kKC;
+  const int nck = (K + KC - 1) / KC;
   const int nchunk = w < nck ? (nck - w + kLinWaves - 1) / kLinWaves : 0;
-  const uint16_t* wrows[4];
+  const uint16_t* wp[WL];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) wrows[j] = a.w + wrow(4 * j + g4) * K + c * 8;
+  for (int j = 0; j < WL; ++j) wp[j] = a.w + wrow(rr + RPI * j) * K + cc * 8;
+  const uint16_t* xp[AL];
+#pragma unroll
+  for (int j = 0; j < AL; ++j) xp[j] = a.x + (int64_t)(row0 + min(rr + RPI * j, M - 1)) * K + cc * 8;
 
   struct Chunk {
-    u32x4 wv[4];          // weight rows 4j + g4, elements 8c .. 8c+7 of the chunk
-    u32x4 xv[MT][4];      // activation row 16mt + c, elements 32s + 8g4 .. +7
-    u32x4 nv[4];          // RMSNorm weight, elements 32s + 8g4 .. +7
+    u32x4 wv[WL];  // weight rows rr + RPI j
+    u32x4 xv[AL];  // activation rows rr + RPI j
+    u32x4 nv;      // RMSNorm weight
     int k0;
   };
-  // PX: the activation slice of the next chunk is prefetched with its
-  // weights (all but the widest normalising instances, whose registers
-  // would not hold two chunks; those load it when the chunk is multiplied)
-  constexpr bool PX = !(NORM && MT >= 4);
   const u32x4 zero4 = {0u, 0u, 0u, 0u};
-  auto issue_x = [&](Chunk& ch, int k0) {
-    const bool whole = k0 + kKC <= K;  // uniform
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int m = mt * 16 + c;
-      const uint16_t* xr = a.x + (int64_t)(row0 + (m < M ? m : M - 1)) * K + k0 + 8 * g4;
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-        ch.xv[mt][s] = (whole || k0 + 32 * s + 8 * g4 < K) ? *reinterpret_cast<const u32x4*>(xr + 32 * s) : zero4;
-    }
-    if constexpr (NORM) {
-#pragma unroll
-      for (int s = 0; s < 4; ++s)
-        ch.nv[s] = (whole || k0 + 32 * s + 8 * g4 < K) ? *reinterpret_cast<const u32x4*>(a.norm_w + k0 + 32 * s + 8 * g4)
-                                                        : zero4;
-    }
-  };
   auto issue = [&](Chunk& ch, int k0) {
-    const bool whole = k0 + kKC <= K;
+    const bool in = k0 + KC <= K || k0 + cc * 8 < K;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-      ch.wv[j] = (whole || k0 + c * 8 < K) ? *reinterpret_cast<const u32x4*>(wrows[j] + k0) : zero4;
+    for (int j = 0; j < WL; ++j) ch.wv[j] = in ? *reinterpret_cast<const u32x4*>(wp[j] + k0) : zero4;
+#pragma unroll
+    for (int j = 0; j < AL; ++j) ch.xv[j] = in ? *reinterpret_cast<const u32x4*>(xp[j] + k0) : zero4;
+    if constexpr (NORM) ch.nv = in ? *reinterpret_cast<const u32x4*>(a.norm_w + k0 + cc * 8) : zero4;
     ch.k0 = k0;
-    if constexpr (PX) issue_x(ch, k0);
   };
 
-  uint16_t* wst = reinterpret_cast<uint16_t*>(smem) + w * kBN * kWStr;
+  uint16_t* st = reinterpret_cast<uint16_t*>(smem) + w * (kBN + MP) * STR;  // [16 weight + MP activation rows][STR]
   f32x4 acc[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  float rowinv[MT];  // 1 / rms of each row of the lane's row tiles (RMSNorm prologue)
-  auto compute = [&](Chunk& ch) {
-    if constexpr (!PX) issue_x(ch, ch.k0);
-    // stage the 16 weight rows of the chunk (this wave's LDS rows)
+  auto compute = [&](const Chunk& ch) {
+    // stage the chunk's rows (this wave's LDS rows; a wave's LDS ops complete
+    // in order).  RMSNorm prologue: the weight rows take the norm weight,
+    // W'[n][k] = bf16(W[n][k] * norm_w[k]), and 1 / rms scales each output
+    // row at the end -- h W^T = inv * (r W'^T) -- which touches 16 rows per
+    // chunk instead of every activation row.
 #pragma unroll
-    for (int j = 0; j < 4; ++j) *reinterpret_cast<u32x4*>(wst + (4 * j + g4) * kWStr + c * 8) = ch.wv[j];
+    for (int j = 0; j < WL; ++j) {
+      u32x4 v = ch.wv[j];
+      if constexpr (NORM) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          v[q] = pack_bf16x2(bfv(v[q], 0) * bfv(ch.nv[q], 0), bfv(v[q], 1) * bfv(ch.nv[q], 1));
+      }
+      *reinterpret_cast<u32x4*>(st + (rr + RPI * j) * STR + cc * 8) = v;
+    }
+#pragma unroll
+    for (int j = 0; j < AL; ++j) {
+      const int m = rr + RPI * j;
+      *reinterpret_cast<u32x4*>(st + (kBN + m) * STR + cc * 8) = m < M ? ch.xv[j] : zero4;
+    }
     __builtin_amdgcn_wave_barrier();
+    // operand reads: lane (g4, c) takes row c, elements 32 s + 8 g4 .. +7
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const u32x4 bw = *reinterpret_cast<const u32x4*>(wst + c * kWStr + 32 * s + 8 * g4);
+    for (int s = 0; s < KC / 32; ++s) {
+      const u32x4 bw = *reinterpret_cast<const u32x4*>(st + c * STR + 32 * s + 8 * g4);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        u32x4 av = ch.xv[mt][s];
-        if (mt * 16 + c >= M) av = u32x4{0u, 0u, 0u, 0u};
-        if constexpr (NORM) {
-          // h = bf16(r * inv * norm_w), the RMSNorm output the projection consumes
-          uint32_t o[4];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            const float h0 = bfv(av[q], 0) * rowinv[mt] * bfv(ch.nv[s][q], 0);
-            const float h1 = bfv(av[q], 1) * rowinv[mt] * bfv(ch.nv[s][q], 1);
-            o[q] = (uint32_t)f32_to_bf16_bits(h0) | ((uint32_t)f32_to_bf16_bits(h1) << 16);
-          }
-          av = u32x4{o[0], o[1], o[2], o[3]};
-        }
+        const u32x4 av = *reinterpret_cast<const u32x4*>(st + (kBN + mt * 16 + c) * STR + 32 * s + 8 * g4);
         acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(to_bf16x8(av), to_bf16x8(bw), acc[mt], 0, 0, 0);
       }
     }
@@ -163,8 +163,8 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinearArgs a) {
 
   // ---- two-stage pipeline over this wave's chunks
   Chunk A, B;
-  auto k_of = [&](int i) { return (w + i * kLinWaves) * kKC; };
-  if (nchunk > 0) issue(A, k_of(0));  // the first weights stream in during the prologue below
+  auto k_of = [&](int i) { return (w + i * kLinWaves) * KC; };
+  if (nchunk > 0) issue(A, k_of(0));  // the first chunk streams in during the prologue below
 
   // ---- RMSNorm prologue: 1 / rms per row from the producer's partial sums,
   // added in a fixed order (thread part p sums slots p, p + P, ...; row m
@@ -173,8 +173,16 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinearArgs a) {
     constexpr int P = kLinThreads / MP;
     const int m = tid % MP, p = tid / MP;
     float s = 0.f;
-    if (p < P && m < M)
-      for (int j = p; j < a.nss_in; j += P) s += a.ss_in[(int64_t)j * a.M + row0 + m];
+    if (p < P && m < M) {
+      const float* src = a.ss_in + row0 + m;
+      for (int j0 = p; j0 < a.nss_in; j0 += 8 * P) {  // 8 loads in flight per round trip
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = j0 + u * P < a.nss_in ? src[(int64_t)(j0 + u * P) * a.M] : 0.f;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) s += v[u];
+      }
+    }
     ss_s[tid] = s;
     __syncthreads();
     if (tid < MP) {
@@ -184,9 +192,6 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinearArgs a) {
     }
     __syncthreads();
   }
-
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt) rowinv[mt] = NORM ? inv_s[mt * 16 + c] : 1.f;
 
   for (int i = 0; i < nchunk; i += 2) {
     if (i + 1 < nchunk) issue(B, k_of(i + 1));
@@ -209,7 +214,7 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinearArgs a) {
     float v = 0.f;
 #pragma unroll
     for (int ww = 0; ww < kLinWaves; ++ww) v += red[(ww * MP + m) * (kBN + 1) + col];
-    return v;
+    return NORM ? v * inv_s[m] : v;
   };
   if constexpr (EPI == 1) {
     // item = (row, 4 gate columns): silu(gate) * up for 4 outputs

