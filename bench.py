@@ -136,11 +136,11 @@ def config3_prompts(batch: int, seed: int = 3, prefix: int = 1200, span: int = 4
     return [doc + spans[(b * 5 + 1) % nspans][:6] for b in range(batch)]
 
 
-def e2e_round(batches=(1, 8), tokens: int = 48, K: int = 8) -> dict:
+def e2e_round(batches=(1, 2, 4, 8), tokens: int = 48, K: int = 8) -> dict:
     """the whole greedy n-gram verification round of a
-    random-init Qwen3-0.6B (28 layers, bf16), one hipGraph replay per round
-    per batch bucket; decode tokens per second over the rounds (prefill
-    excluded, reported apart)."""
+    random-init Qwen3-0.6B (28 layers, bf16) at batch 1/2/4/8, one hipGraph
+    replay per round per batch bucket; decode tokens per second over the
+    rounds (prefill excluded, reported apart)."""
     from naivllm_amd.sampling_parameters import SamplingParams
     from naivllm_amd.spec_engine.spec_llm_engine import SpecLLMEngine
 

@@ -283,12 +283,18 @@ int nsv_silu_mul(const void* gate_up, void* out, int T, int I, void* stream);
  *   epilogue 2 (the residual add of layernorm.py:29-31): resid [M, N] =
  *     bf16(h W^T) + resid, and ss_out [N/16, M] receives the partial sums
  *     of the new resid^2 over each 16-column tile; y is unused.
- * N % 16 == 0, K % 8 == 0.
+ * N % 16 == 0, K % 8 == 0.  For 32-80 rows and fewer than 128 column tiles
+ * the reduction is split over up to 4 workgroups per tile, whose partials
+ * meet in `workspace` (nsv_linear_workspace_size bytes, zero-filled before
+ * the first call; every call leaves its counters at zero again, so one
+ * workspace serves every call on a stream); otherwise no workspace is used.
  */
+size_t nsv_linear_workspace_size(int M, int N, int K);
 int nsv_linear(const void* x, const void* norm_w, const float* ss_in,
                int nss_in, float eps, const void* weight, void* y,
                void* resid, float* ss_out, int M, int N, int K,
-               int epilogue, void* stream);
+               int epilogue, void* workspace, size_t workspace_bytes,
+               void* stream);
 
 #ifdef __cplusplus
 }

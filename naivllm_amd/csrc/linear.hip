@@ -50,6 +50,9 @@ struct LinearArgs {
   uint16_t* resid;         // [M, N] residual stream, read and rewritten (residual epilogue)
   float* ss_out;           // [N/16, M] partial sums of r^2 (residual epilogue)
   int M, N, K;
+  int ks;                  // workgroups per 16-column tile, each taking a share of the reduction
+  float* part;             // [N/16, ks, 80, 16] their partial products (ks > 1)
+  unsigned* counters;      // [N/16] tile workgroups done so far; every call leaves them zero
 };
 
 __device__ __forceinline__ bf16x8 to_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
@@ -78,6 +81,7 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinearArgs a) {
   __shared__ float ss_s[kLinThreads];
 
   const int tile = blockIdx.x;
+  const int kz = blockIdx.z;  // this workgroup's share of the reduction (split-K)
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g4 = lane >> 4, c = lane & 15;
@@ -93,10 +97,12 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinearArgs a) {
     if constexpr (EPI == 1) return col < 8 ? tile * 8 + col : half + tile * 8 + (col - 8);
     else return (int64_t)tile * kBN + col;
   };
-  // the reduction in chunks of KC elements, dealt to the waves round-robin
-  // (chunk w + 8i is wave w's i-th); a last partial chunk reads zeros past K
+  // the reduction in chunks of KC elements, dealt round-robin to the
+  // ks * 8 waves of the tile (worker u = 8 kz + w takes chunks u, u + 8 ks,
+  // ...); a last partial chunk reads zeros past K
   const int nck = (K + KC - 1) / KC;
-  const int nchunk = w < nck ? (nck - w + kLinWaves - 1) / kLinWaves : 0;
+  const int worker = kz * kLinWaves + w, nworkers = a.ks * kLinWaves;
+  const int nchunk = worker < nck ? (nck - worker + nworkers - 1) / nworkers : 0;
   const uint16_t* wp[WL];
 #pragma unroll
   for (int j = 0; j < WL; ++j) wp[j] = a.w + wrow(rr + RPI * j) * K + cc * 8;
@@ -163,7 +169,7 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinearArgs a) {
 
   // ---- two-stage pipeline over this wave's chunks
   Chunk A, B;
-  auto k_of = [&](int i) { return (w + i * kLinWaves) * KC; };
+  auto k_of = [&](int i) { return (worker + i * nworkers) * KC; };
   if (nchunk > 0) issue(A, k_of(0));  // the first chunk streams in during the prologue below
 
   // ---- RMSNorm prologue: 1 / rms per row from the producer's partial sums,
@@ -210,6 +216,58 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinearArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) red[(w * MP + mt * 16 + g4 * 4 + i) * (kBN + 1) + c] = acc[mt][i];
   __syncthreads();
+  if (a.ks > 1) {
+    // ---- split-K: publish this workgroup's tile partial; the tile's last
+    // workgroup to finish sums the ks partials in order (deterministic) and
+    // runs the epilogue.  Partials and the arrival counter are agent-scope
+    // (coherent across XCDs without cache maintenance).
+    const int m = tid >> 2, q = tid & 3;
+    float* pt = a.part + (int64_t)tile * a.ks * (kMaxRows * kBN);
+    if (tid < MP * 4 && m < M) {
+      float v[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        v[e] = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < kLinWaves; ++ww) v[e] += red[(ww * MP + m) * (kBN + 1) + 4 * q + e];
+      }
+      uint64_t* dst = reinterpret_cast<uint64_t*>(pt + (int64_t)kz * (kMaxRows * kBN) + m * kBN + 4 * q);
+      __hip_atomic_store(dst, (uint64_t)__float_as_uint(v[0]) | ((uint64_t)__float_as_uint(v[1]) << 32),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(dst + 1, (uint64_t)__float_as_uint(v[2]) | ((uint64_t)__float_as_uint(v[3]) << 32),
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    __shared__ int last;
+    if (tid == 0)
+      last = __hip_atomic_fetch_add(&a.counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+             (unsigned)(a.ks - 1);
+    __syncthreads();
+    if (!last) return;
+    if (tid == 0) __hip_atomic_store(&a.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // the tile's total into wave 0's slot of red, zeros in the others, so the
+    // epilogue below reads it unchanged
+    if (tid < MP * 4 && m < M) {
+      float v[4] = {0.f, 0.f, 0.f, 0.f};
+      for (int z = 0; z < a.ks; ++z) {
+        const uint64_t* src = reinterpret_cast<const uint64_t*>(pt + (int64_t)z * (kMaxRows * kBN) + m * kBN + 4 * q);
+        const uint64_t lo = __hip_atomic_load(const_cast<uint64_t*>(src), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint64_t hi = __hip_atomic_load(const_cast<uint64_t*>(src + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        v[0] += __uint_as_float((uint32_t)lo);
+        v[1] += __uint_as_float((uint32_t)(lo >> 32));
+        v[2] += __uint_as_float((uint32_t)hi);
+        v[3] += __uint_as_float((uint32_t)(hi >> 32));
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        red[m * (kBN + 1) + 4 * q + e] = v[e];
+#pragma unroll
+        for (int ww = 1; ww < kLinWaves; ++ww) red[(ww * MP + m) * (kBN + 1) + 4 * q + e] = 0.f;
+      }
+    }
+    __syncthreads();
+  }
   auto colsum = [&](int m, int col) {
     float v = 0.f;
 #pragma unroll
@@ -285,21 +343,52 @@ int launch_linear(const LinearArgs& a, bool norm, int epi, dim3 grid, hipStream_
   return nsv_launch_status();
 }
 
+// Workgroups per 16-column tile: a split of the reduction when the tiles
+// alone leave most of the chip idle and there are enough rows to amortise
+// the partial exchange (measured: the exchange costs more than it saves at
+// one or two 16-row tiles).
+int linear_splits(int M, int N, int K) {
+  const int tiles = N / kBN;
+  if (M < 32 || M > kMaxRows || tiles >= 128) return 1;
+  int ks = 256 / tiles;
+  ks = ks > 4 ? 4 : (ks < 1 ? 1 : ks);
+  while (ks > 1 && K < ks * kLinWaves * 64) --ks;  // every worker keeps a chunk
+  return ks;
+}
+
+size_t linear_ws_bytes(int M, int N, int K) {
+  const int ks = linear_splits(M, N, K);
+  if (ks <= 1) return 0;
+  const size_t tiles = (size_t)(N / kBN);
+  return ((tiles * sizeof(unsigned) + 255) & ~(size_t)255) + tiles * ks * kMaxRows * kBN * sizeof(float);
+}
+
 }  // namespace
 
 extern "C" {
 
+size_t nsv_linear_workspace_size(int M, int N, int K) {
+  if (M <= 0 || N <= 0 || K <= 0 || N % kBN) return 0;
+  return linear_ws_bytes(M, N, K);
+}
+
 int nsv_linear(const void* x, const void* norm_w, const float* ss_in, int nss_in, float eps, const void* weight,
-               void* y, void* resid, float* ss_out, int M, int N, int K, int epilogue, void* stream) {
+               void* y, void* resid, float* ss_out, int M, int N, int K, int epilogue, void* workspace,
+               size_t workspace_bytes, void* stream) {
   if (M < 0 || N <= 0 || K <= 0 || epilogue < 0 || epilogue > 2) return NSV_ERR_ARG;
   if (M == 0) return NSV_OK;
   if (N % kBN || K % 8 || M > 65535 * kMaxRows) return NSV_ERR_UNSUPPORTED;
   if (!x || !weight) return NSV_ERR_ARG;
   if (norm_w && (!ss_in || nss_in <= 0)) return NSV_ERR_ARG;
   if (epilogue == 2 ? (!resid || !ss_out) : !y) return NSV_ERR_ARG;
+  const int ks = linear_splits(M, N, K);
+  const size_t need = linear_ws_bytes(M, N, K);
+  if (need && (!workspace || workspace_bytes < need)) return NSV_ERR_WORKSPACE;
+  const size_t cnt = ((size_t)(N / kBN) * sizeof(unsigned) + 255) & ~(size_t)255;
   LinearArgs a{(const uint16_t*)x, (const uint16_t*)norm_w, ss_in, nss_in, eps, (const uint16_t*)weight,
-               (uint16_t*)y, (uint16_t*)resid, ss_out, M, N, K};
-  const dim3 grid(N / kBN, (M + kMaxRows - 1) / kMaxRows);
+               (uint16_t*)y, (uint16_t*)resid, ss_out, M, N, K, ks,
+               need ? (float*)((char*)workspace + cnt) : nullptr, need ? (unsigned*)workspace : nullptr};
+  const dim3 grid(N / kBN, (M + kMaxRows - 1) / kMaxRows, ks);
   hipStream_t s = (hipStream_t)stream;
   const bool norm = norm_w != nullptr;
   switch ((min(M, kMaxRows) + 15) / 16) {

@@ -103,9 +103,12 @@ def linear(x: torch.Tensor, weight: torch.Tensor, y: torch.Tensor | None = None,
     N = weight.shape[0]
     epi = 2 if resid is not None else (1 if swiglu else 0)
     nss = ss_in.shape[0] if ss_in is not None else 0
-    rc = _lib.lib().nsv_linear(x.data_ptr(), _lib.ptr(norm_w), _lib.ptr(ss_in), nss, eps, weight.data_ptr(),
-                               _lib.ptr(y), _lib.ptr(resid), _lib.ptr(ss_out), M, N, K, epi,
-                               _lib.stream_ptr(x.device))
+    h = _lib.lib()
+    nbytes = h.nsv_linear_workspace_size(M, N, K)
+    ws = _lib.workspace(x.device, nbytes, "linear")
+    rc = h.nsv_linear(x.data_ptr(), _lib.ptr(norm_w), _lib.ptr(ss_in), nss, eps, weight.data_ptr(),
+                      _lib.ptr(y), _lib.ptr(resid), _lib.ptr(ss_out), M, N, K, epi, _lib.ptr(ws),
+                      ws.numel() if ws is not None else 0, _lib.stream_ptr(x.device))
     _lib.check(rc, "linear")
 
 

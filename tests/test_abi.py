@@ -131,11 +131,17 @@ def test_accept_and_ngram_reject_bad_arguments_before_launch():
 
 def test_linear_rejects_bad_arguments_before_launch():
     h = _lib.lib()
-    # x, norm_w, ss_in, nss_in, eps, weight, y, resid, ss_out, M, N, K, epilogue, stream
-    assert h.nsv_linear(1, None, None, 0, 1e-6, 1, 1, None, None, 9, 1000, 1024, 0, None) == -2  # N % 16
-    assert h.nsv_linear(1, None, None, 0, 1e-6, 1, 1, None, None, 9, 1024, 1020, 0, None) == -2  # K % 8
-    assert h.nsv_linear(None, None, None, 0, 1e-6, 1, 1, None, None, 9, 1024, 1024, 0, None) == -1
-    assert h.nsv_linear(1, None, None, 0, 1e-6, 1, 1, None, None, 9, 1024, 1024, 3, None) == -1
-    assert h.nsv_linear(1, 1, None, 0, 1e-6, 1, 1, None, None, 9, 1024, 1024, 0, None) == -1  # norm without sums
-    assert h.nsv_linear(1, None, None, 0, 1e-6, 1, None, None, None, 9, 1024, 1024, 2, None) == -1  # no stream
-    assert h.nsv_linear(1, None, None, 0, 1e-6, 1, 1, None, None, 0, 1024, 1024, 0, None) == 0  # no rows
+    # x, norm_w, ss_in, nss_in, eps, weight, y, resid, ss_out, M, N, K, epilogue, workspace, ws_bytes, stream
+    assert h.nsv_linear(1, None, None, 0, 1e-6, 1, 1, None, None, 9, 1000, 1024, 0, None, 0, None) == -2  # N % 16
+    assert h.nsv_linear(1, None, None, 0, 1e-6, 1, 1, None, None, 9, 1024, 1020, 0, None, 0, None) == -2  # K % 8
+    assert h.nsv_linear(None, None, None, 0, 1e-6, 1, 1, None, None, 9, 1024, 1024, 0, None, 0, None) == -1
+    assert h.nsv_linear(1, None, None, 0, 1e-6, 1, 1, None, None, 9, 1024, 1024, 3, None, 0, None) == -1
+    assert h.nsv_linear(1, 1, None, 0, 1e-6, 1, 1, None, None, 9, 1024, 1024, 0, None, 0, None) == -1  # norm, no sums
+    assert h.nsv_linear(1, None, None, 0, 1e-6, 1, None, None, None, 9, 1024, 1024, 2, None, 0, None) == -1
+    assert h.nsv_linear(1, None, None, 0, 1e-6, 1, 1, None, None, 0, 1024, 1024, 0, None, 0, None) == 0  # no rows
+    # split reduction (72 rows, 64 column tiles) needs the workspace; 9 rows do not
+    assert h.nsv_linear_workspace_size(9, 1024, 2048) == 0
+    n = h.nsv_linear_workspace_size(72, 1024, 2048)
+    assert n >= 64 * 4 * 80 * 16 * 4
+    assert h.nsv_linear(1, None, None, 0, 1e-6, 1, 1, None, None, 72, 1024, 2048, 0, None, 0, None) == -3
+    assert h.nsv_linear_workspace_size(72, 4096, 1024) == 0  # 256 tiles cover the chip without a split

@@ -80,7 +80,7 @@ def test_linear_plain(M, N, K, norm):
         torch.testing.assert_close(y.float(), x.float() @ w.float().t(), **BF16)
 
 
-@pytest.mark.parametrize("M,I,K", [(9, 3072, 1024), (72, 3072, 1024), (5, 128, 256), (90, 256, 512)])
+@pytest.mark.parametrize("M,I,K", [(9, 3072, 1024), (72, 3072, 1024), (5, 128, 256), (90, 256, 512), (40, 256, 1024)])
 def test_linear_swiglu(M, I, K):
     print(f"case: linear swiglu M={M} I={I} K={K}", flush=True)
     g = gen(M + I + K)
@@ -144,3 +144,31 @@ def test_linear_chain_matches_unfused_layer():
     want = norm_linear_ref(rr.to(torch.bfloat16), ln_f, w_lm, 1e-6)
     rel = (logits.float() - want).norm() / want.norm()
     assert rel < 1e-2, float(rel)
+
+
+@pytest.mark.parametrize("M,N,K", [(72, 1024, 2048), (48, 512, 3072), (33, 1024, 1024)])
+def test_split_reduction_is_deterministic_and_reusable(M, N, K):
+    # shapes whose reduction is split over several workgroups per column tile:
+    # repeated calls on the shared workspace give identical bits (fixed-order
+    # partial sums, counters left at zero), for every epilogue
+    print(f"case: split-K linear M={M} N={N} K={K}", flush=True)
+    from naivllm_amd import _lib
+    assert _lib.lib().nsv_linear_workspace_size(M, N, K) > 0
+    g = gen(M + N + K)
+    x = randn(g, M, K)
+    w = randn(g, N, K, scale=K ** -0.5)
+    ys = [torch.empty(M, N, dtype=torch.bfloat16, device="cuda") for _ in range(3)]
+    for y in ys:
+        qm.linear(x, w, y)
+    assert torch.equal(ys[0], ys[1]) and torch.equal(ys[1], ys[2])
+    torch.testing.assert_close(ys[0].float(), x.float() @ w.float().t(), **BF16)
+    r0 = randn(g, M, N)
+    outs = []
+    for _ in range(2):
+        r = r0.clone()
+        ss = torch.empty(N // 16, M, device="cuda")
+        qm.linear(x, w, resid=r, ss_out=ss)
+        outs.append((r, ss))
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    prod = (x.float() @ w.float().t()).to(torch.bfloat16)
+    torch.testing.assert_close(outs[0][0].float(), (prod.float() + r0.float()).to(torch.bfloat16).float(), **BF16)
