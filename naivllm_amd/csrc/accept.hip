@@ -139,10 +139,36 @@ __global__ __launch_bounds__(kThreads) void greedy_argmax_kernel(GreedyArgs a) {
   const int b = rowid / (a.K + 1), r = rowid - b * (a.K + 1);
   const int kb = min(max(a.num_drafts[b], 0), a.K);
   if (r > kb) return;  // uniform: a row the sequence does not use
-  const Chunk c = chunk_of(ch, a.nch, a.V);
+  // chunks of a multiple of 8 elements, so that 16-byte loads stay aligned
+  // (the maximum does not depend on how the row is cut)
+  const int64_t per = (((int64_t)a.V + a.nch - 1) / a.nch + 7) & ~(int64_t)7;
   const int64_t base = ((int64_t)b * a.seq_stride + r) * a.V;
   uint64_t best = 0;
-  for (int64_t v = c.lo + threadIdx.x; v < c.hi; v += kThreads) {
+  int64_t lo = min((int64_t)a.V, ch * per), hi = min((int64_t)a.V, lo + per);
+  if (a.dtype == NSV_BF16 && ((base + lo) & 7) == 0) {
+    // 8 elements per 16-byte load, two loads in flight per iteration; the
+    // rest of the chunk (fewer than 8 elements) below
+    const int64_t nvec = (hi - lo) >> 3;
+    const u32x4* src = reinterpret_cast<const u32x4*>((const uint16_t*)a.logits + base + lo);
+    for (int64_t j = threadIdx.x; j < nvec; j += 2 * kThreads) {
+      u32x4 w[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u) w[u] = j + u * kThreads < nvec ? src[j + u * kThreads] : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        if (j + u * kThreads >= nvec) break;
+        const uint32_t v0 = (uint32_t)(lo + ((j + u * kThreads) << 3));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t bits = (e & 1) ? (w[u][e >> 1] >> 16) : (w[u][e >> 1] & 0xffffu);
+          const uint64_t k = argmax_key(bf16_bits_to_f32(bits), v0 + e);
+          best = k > best ? k : best;
+        }
+      }
+    }
+    lo += nvec << 3;
+  }
+  for (int64_t v = lo + threadIdx.x; v < hi; v += kThreads) {
     const uint64_t k = argmax_key(load_elem(a.logits, base + v, a.dtype), (uint32_t)v);
     best = k > best ? k : best;
   }
