@@ -4,11 +4,10 @@
 // The verify forward multiplies B*(K+1) activation rows (72 at batch 8) by weight
 // matrices of 2-300 MB, so streaming the weights, not arithmetic, bounds
 // every projection.  A workgroup owns 16 output columns (16 weight rows):
-// its 8 waves take 64- or 128-element chunks of the reduction dimension in
-// turn,
-// load their slice of the 16
-// rows and of every activation row as whole-row 16-byte loads (8 or 16
-// lanes cover one row's contiguous chunk), reshape both through a per-wave
+// its 8 waves take 32- to 128-element chunks of the reduction dimension in
+// turn, load their slice of the 16 rows and of every activation row as
+// whole-row 16-byte loads (4 or 8 lanes cover one row's contiguous chunk),
+// reshape both through a per-wave
 // LDS tile into the MFMA operand layout and multiply them
 // (v_mfma_f32_16x16x32_bf16, rows padded to 16; more than 80 rows take
 // further workgroup rows of the grid); the waves' partial
@@ -64,10 +63,19 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 }
 __device__ __forceinline__ float bfv(uint32_t word, int hi) { return __uint_as_float(hi ? (word & 0xffff0000u) : (word << 16)); }
 
-template <int MT, bool NORM, int EPI>  // EPI 0: plain, 1: SwiGLU, 2: residual
-__global__ __launch_bounds__(kLinThreads) void linear_kernel(LinearArgs a) {
+// Chunk size and occupancy.  A grid of more workgroups than CUs (384 for
+// gate_up) needs two resident per CU, or its last third starts only when
+// the first workgroups end.  Measured on MI355X, two 8-wave workgroups share
+// a CU at <= 64 KB of LDS each (61 KB did, 70 KB did not) and <= 128 VGPRs
+// per lane: the small chunk (64 elements up to 32 rows, 32 beyond) keeps the
+// per-wave staging of [16 + MP rows][KC] within that.  A grid that fits the
+// CUs takes twice the chunk (half the round trips of a long reduction).
+constexpr int lin_kc(int MT, bool small) { return (MT <= 2 ? 128 : 64) / (small ? 2 : 1); }
+
+template <int MT, bool NORM, int EPI, bool SMALL>  // EPI 0: plain, 1: SwiGLU, 2: residual
+__global__ __launch_bounds__(kLinThreads, SMALL ? 2 : 1) void linear_kernel(LinearArgs a) {
   constexpr int MP = MT * 16;
-  constexpr int KC = MT <= 2 ? 128 : 64;  // reduction elements per wave chunk (LDS holds 8 waves' chunks)
+  constexpr int KC = lin_kc(MT, SMALL);   // reduction elements per wave chunk
   constexpr int LPR = KC / 8;             // lanes per row of a whole-row load (16 bytes each)
   constexpr int RPI = 64 / LPR;           // rows per load instruction
   constexpr int STR = KC + 8;             // staged row stride (bf16): 16-byte reads of 16 rows hit distinct banks
@@ -327,9 +335,29 @@ __global__ __launch_bounds__(kLinThreads) void linear_kernel(LinearArgs a) {
   }
 }
 
-template <int MT>
-int launch_linear(const LinearArgs& a, bool norm, int epi, dim3 grid, hipStream_t s) {
-#define NSV_LIN(NORM, EPI) hipLaunchKernelGGL((linear_kernel<MT, NORM, EPI>), grid, dim3(kLinThreads), 0, s, a)
+// Compute units of the current device (256 on MI355X), queried once per
+// device; a failed query assumes 256.
+int lin_device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) {
+    (void)hipGetLastError();
+    return 256;
+  }
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) {
+      (void)hipGetLastError();
+      cus = 256;
+    }
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
+template <int MT, bool SMALL>
+int launch_linear_kc(const LinearArgs& a, bool norm, int epi, dim3 grid, hipStream_t s) {
+#define NSV_LIN(NORM, EPI) hipLaunchKernelGGL((linear_kernel<MT, NORM, EPI, SMALL>), grid, dim3(kLinThreads), 0, s, a)
   if (norm) {
     if (epi == 0) NSV_LIN(true, 0);
     else if (epi == 1) NSV_LIN(true, 1);
@@ -343,6 +371,12 @@ int launch_linear(const LinearArgs& a, bool norm, int epi, dim3 grid, hipStream_
   return nsv_launch_status();
 }
 
+template <int MT>
+int launch_linear(const LinearArgs& a, bool norm, int epi, dim3 grid, hipStream_t s) {
+  if ((int64_t)grid.x * grid.y * grid.z > lin_device_cus()) return launch_linear_kc<MT, true>(a, norm, epi, grid, s);
+  return launch_linear_kc<MT, false>(a, norm, epi, grid, s);
+}
+
 // Workgroups per 16-column tile: a split of the reduction when the tiles
 // alone leave most of the chip idle and there are enough rows to amortise
 // the partial exchange (measured: the exchange costs more than it saves at
@@ -352,7 +386,7 @@ int linear_splits(int M, int N, int K) {
   if (M < 32 || M > kMaxRows || tiles >= 128) return 1;
   int ks = 256 / tiles;
   ks = ks > 4 ? 4 : (ks < 1 ? 1 : ks);
-  while (ks > 1 && K < ks * kLinWaves * 64) --ks;  // every worker keeps a chunk
+  while (ks > 1 && K < ks * kLinWaves * 64) --ks;  // every worker keeps a chunk of the larger size
   return ks;
 }
 
