@@ -248,7 +248,9 @@ int nsv_commit(const int32_t* tokens, const int32_t* num_tokens,
  *   [D]), NeoX rotation at positions[t] from cos_sin [max_pos, D] (fp32,
  *   cos then sin), q written to q_out [T, H, D], k and v stored into the
  *   paged caches at slot_mapping[t] (slot < 0: not stored).  D even,
- *   <= 128.  Replaces models/qwen3.py:100-119 + layers/rotary_embedding.py:
+ *   <= 128.  positions == NULL: cos_sin holds one row per step row
+ *   ([T, D], the table gathered at the rows' positions; max_pos >= T).
+ *   Replaces models/qwen3.py:100-119 + layers/rotary_embedding.py:
  *   78-86 + layers/attention.py:71-112.
  * nsv_silu_mul: out [T, I] = silu(gate_up[:, :I]) * gate_up[:, I:].
  *   Replaces layers/activation.py:17-19.

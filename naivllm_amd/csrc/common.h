@@ -40,6 +40,29 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Per-head q/k RMSNorm and NeoX rotation of one rotation pair (x1, x2) =
+// (row[l], row[l + D/2]), with floating-point contraction off: every caller
+// evaluates the same IEEE operations (no fused multiply-add chosen per call
+// site), so a row comes out bit-identical wherever it is computed.
+__device__ __forceinline__ float head_sq(float x1, float x2) {
+#pragma clang fp contract(off)
+  return x1 * x1 + x2 * x2;
+}
+__device__ __forceinline__ float head_inv_rms(float sum_sq, int D, float eps) {
+#pragma clang fp contract(off)
+  return rsqrtf(sum_sq / (float)D + eps);
+}
+// The normalised pair is rounded to bf16 (the reference's q_norm / k_norm
+// output) before the rotation by the row's (cos, sin).
+__device__ __forceinline__ void head_norm_rope(float x1, float x2, float inv, float w1, float w2, float c, float s,
+                                               uint16_t& o1, uint16_t& o2) {
+#pragma clang fp contract(off)
+  const float y1 = bf16_bits_to_f32(f32_to_bf16_bits(x1 * inv * w1));
+  const float y2 = bf16_bits_to_f32(f32_to_bf16_bits(x2 * inv * w2));
+  o1 = f32_to_bf16_bits(y1 * c - y2 * s);
+  o2 = f32_to_bf16_bits(y1 * s + y2 * c);
+}
+
 static inline int nsv_launch_status() {
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? NSV_OK : (int)e;

@@ -66,12 +66,14 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_residual_kernel(
 // pair), D/2 <= 64.  q heads: RMSNorm * q_w, rotate, write q_out [T, H, D].
 // k heads: RMSNorm * k_w, rotate, store at the row's slot.  v heads: store.
 // Rows with slot < 0 store nothing; rows with position < 0 use position 0.
+// With positions == NULL the rotary table holds one row per step row
+// ([T, D], gathered at the rows' positions by the caller).
 // ---------------------------------------------------------------------------
 struct EpilogueArgs {
   const uint16_t* qkv;
   const uint16_t* q_w;
   const uint16_t* k_w;
-  const float* cos_sin;  // [max_pos, D]: cos in [0, D/2), sin in [D/2, D)
+  const float* cos_sin;  // [max_pos, D]: cos in [0, D/2), sin in [D/2, D); [T, D] by row without positions
   const int64_t* positions;
   const int64_t* slots;
   uint16_t* q_out;
@@ -102,18 +104,14 @@ __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(EpilogueArgs a)
     return;
   }
   const bool is_q = head < a.H;
-  const float ms = wave_sum(x1 * x1 + x2 * x2) / (float)a.D;
-  const float inv = rsqrtf(ms + a.eps);
+  const float inv = head_inv_rms(wave_sum(head_sq(x1, x2)), a.D, a.eps);
   const uint16_t* w = is_q ? a.q_w : a.k_w;
   if (on) {
-    // the normalised value is bf16 in the reference (q_norm/k_norm output)
-    x1 = bf16_bits_to_f32(f32_to_bf16_bits(x1 * inv * bf(w[lane])));
-    x2 = bf16_bits_to_f32(f32_to_bf16_bits(x2 * inv * bf(w[lane + half])));
-    int64_t pos = a.positions[row];
+    int64_t pos = a.positions ? a.positions[row] : row;
     pos = pos < 0 ? 0 : (pos >= a.max_pos ? a.max_pos - 1 : pos);
     const float c = a.cos_sin[pos * a.D + lane], s = a.cos_sin[pos * a.D + half + lane];
-    const uint16_t o1 = f32_to_bf16_bits(x1 * c - x2 * s);
-    const uint16_t o2 = f32_to_bf16_bits(x1 * s + x2 * c);
+    uint16_t o1, o2;
+    head_norm_rope(x1, x2, inv, bf(w[lane]), bf(w[lane + half]), c, s, o1, o2);
     if (is_q) {
       uint16_t* dst = a.q_out + ((int64_t)row * a.H + head) * a.D;
       dst[lane] = o1;
@@ -160,8 +158,9 @@ int nsv_qk_norm_rope_store(const void* qkv, const void* q_norm_w, const void* k_
                            void* k_cache, void* v_cache, int T, int H, int Hkv, int D, float eps, void* stream) {
   if (T < 0 || H <= 0 || Hkv <= 0 || D <= 0 || (D & 1) || D > 128 || max_pos <= 0) return NSV_ERR_ARG;
   if (T == 0) return NSV_OK;
-  if (!qkv || !q_norm_w || !k_norm_w || !cos_sin || !positions || !slot_mapping || !q_out || !k_cache || !v_cache)
+  if (!qkv || !q_norm_w || !k_norm_w || !cos_sin || !slot_mapping || !q_out || !k_cache || !v_cache)
     return NSV_ERR_ARG;
+  if (!positions && max_pos < T) return NSV_ERR_ARG;  // the per-row table has a row per step row
   EpilogueArgs a{(const uint16_t*)qkv, (const uint16_t*)q_norm_w, (const uint16_t*)k_norm_w, cos_sin, positions,
                  slot_mapping, (uint16_t*)q_out, (uint16_t*)k_cache, (uint16_t*)v_cache, T, H, Hkv, D, max_pos, eps};
   const int64_t waves = (int64_t)T * (H + 2 * Hkv);

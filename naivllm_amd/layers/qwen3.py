@@ -82,9 +82,11 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, out: torch.Tenso
 
 def qk_norm_rope_store(qkv, q_norm_w, k_norm_w, cos_sin, positions, slot_mapping, q_out, k_cache, v_cache,
                        H: int, Hkv: int, D: int, eps: float) -> None:
+    """The pre-attention epilogue (nsv_qk_norm_rope_store).  positions None:
+    cos_sin holds the rotary row of each step row ([T, D])."""
     rc = _lib.lib().nsv_qk_norm_rope_store(
         qkv.data_ptr(), q_norm_w.data_ptr(), k_norm_w.data_ptr(), cos_sin.data_ptr(), cos_sin.shape[0],
-        positions.data_ptr(), slot_mapping.data_ptr(), q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
+        _lib.ptr(positions), slot_mapping.data_ptr(), q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(),
         qkv.shape[0], H, Hkv, D, eps, _lib.stream_ptr(qkv.device))
     _lib.check(rc, "qk_norm_rope_store")
 
@@ -207,12 +209,16 @@ class Qwen3Verify:
             act = torch.empty(T, I, dtype=self.dtype, device=self.device)
             ss_o = torch.empty(E // 16, T, dtype=torch.float32, device=self.device)  # partial sums of resid^2
             ss_d = torch.empty(E // 16, T, dtype=torch.float32, device=self.device)
+            # the rotary rows of the step's positions, gathered once for every layer
+            # (position < 0 takes row 0, as the epilogue kernel does), so that each
+            # layer's epilogue loads them without first loading the positions
+            rope_rows = self.rope.index_select(0, positions.clamp(0, self.rope.shape[0] - 1))
             for li, L in enumerate(self.layers):
                 if li == 0:
                     linear(h, L["qkv"], qkv)
                 else:
                     linear(resid, L["qkv"], qkv, norm_w=L["ln1"], ss_in=ss_d, eps=eps)
-                qk_norm_rope_store(qkv, L["q_norm"], L["k_norm"], self.rope, positions, slot_mapping, q,
+                qk_norm_rope_store(qkv, L["q_norm"], L["k_norm"], rope_rows, None, slot_mapping, q,
                                    self.k_caches[li], self.v_caches[li], H, Hkv, D, eps)
                 linear(attn(li).view(T, H * D), L["o"], resid=resid, ss_out=ss_o)
                 linear(resid, L["gate_up"], act, norm_w=L["ln2"], ss_in=ss_o, eps=eps, swiglu=True)

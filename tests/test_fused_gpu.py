@@ -97,6 +97,12 @@ def test_qk_norm_rope_store(D):
     untouched = torch.ones(nb * bs, dtype=torch.bool, device="cuda")
     untouched[slots[stored]] = False
     assert not kflat[untouched].any() and not vflat[untouched].any()
+    # the rotary table gathered per row (positions None; position -1 takes row 0)
+    # gives the same bits as the position lookup
+    rows = cos_sin.index_select(0, positions.clamp(0, cos_sin.shape[0] - 1))
+    q2, kc2, vc2 = torch.zeros_like(q_out), torch.zeros_like(kc), torch.zeros_like(vc)
+    qm.qk_norm_rope_store(qkv, qw, kw, rows, None, slots, q2, kc2, vc2, H, Hkv, D, 1e-6)
+    assert torch.equal(q2, q_out) and torch.equal(kc2, kc) and torch.equal(vc2, vc)
 
 
 @pytest.mark.parametrize("T,I", [(1, 512), (72, 3072), (3, 1000)])
@@ -151,12 +157,13 @@ def dense_forward(model: Qwen3Verify, ids: torch.Tensor) -> torch.Tensor:
     return norm(x, model.norm) @ f(model.lm_head).t()
 
 
-@pytest.mark.parametrize("fused", [True, False])
-def test_forward_matches_dense_fp32(fused, monkeypatch):
+@pytest.mark.parametrize("fused,bs", [(True, 16), (True, 32), (False, 16)])
+def test_forward_matches_dense_fp32(fused, bs, monkeypatch):
     # two sequences: a first chunk written into a fresh paged cache, then a
     # 9-row verify chunk reading it back, against a dense fp32 forward; both
     # the fused few-row path and the hipBLASLt path of wider batches
-    print(f"case: qwen3 verify forward vs dense fp32, fused={fused}", flush=True)
+    # (32-key pages: the 9-row chunk runs the fused epilogue + attention kernel)
+    print(f"case: qwen3 verify forward vs dense fp32, fused={fused} block_size={bs}", flush=True)
     monkeypatch.setattr(qm, "FUSED_ROWS", 1 << 30 if fused else 0)
     monkeypatch.setattr(qm, "FUSED_ROWS_WIDE", 1 << 30 if fused else 0)
     cfg = Qwen3Config(vocab_size=2048, hidden_size=256, num_layers=2, num_heads=4, num_kv_heads=2, head_dim=64,
@@ -166,7 +173,6 @@ def test_forward_matches_dense_fp32(fused, monkeypatch):
     for L in model.layers:  # non-trivial norm weights, so a swapped weight shows
         for key in ("ln1", "ln2", "q_norm", "k_norm"):
             L[key] = (1.0 + 0.3 * torch.randn(L[key].shape, generator=g, device="cuda")).to(torch.bfloat16)
-    bs = 16
     model.allocate_kv_cache(16, bs)
     lens1, lens2 = [20, 7], [9, 9]
     seqs = [torch.randint(0, cfg.vocab_size, (a + b,), generator=g, device="cuda") for a, b in zip(lens1, lens2)]
@@ -193,3 +199,4 @@ def test_forward_matches_dense_fp32(fused, monkeypatch):
         got = torch.cat([first[b], second[b]])
         rel = (got - want).norm() / want.norm()
         assert rel < 2e-2, (b, float(rel))
+
