@@ -118,12 +118,16 @@ class VerifyRound:
         self.max_tokens = torch.zeros(max_batch, **i32)
         self.max_len = torch.zeros(max_batch, **i32)
         self.ignore_eos = torch.zeros(max_batch, **i32)
-        self.active = torch.zeros(max_batch, **i32)
+        # the round's report rows, read back by the host in one transfer: active
+        # flags, tokens committed, tokens drafted, drafts from the model.  The
+        # per-sequence state below is these rows themselves (no copies per round).
+        self.report_dev = torch.zeros(4, max_batch, **i32)
+        self.active = self.report_dev[0]
         self.temperature = torch.zeros(max_batch, dtype=torch.float32, device=dev)
         self.block_tables = torch.full((max_batch, max_blocks), -1, **i32)
         self.drafts = torch.zeros(max_batch, max(K, 1), **i32)
-        self.num_drafts = torch.zeros(max_batch, **i32)
-        self.draft_mode = torch.zeros(max_batch, **i32)  # 1: the sequence's drafts came from the model
+        self.num_drafts = self.report_dev[2]
+        self.draft_mode = self.report_dev[3]  # 1: the sequence's drafts came from the model
         self.input_ids = torch.zeros(rows, **i64)
         self.positions = torch.full((rows,), -1, **i64)
         self.slot_mapping = torch.full((rows,), -1, **i64)
@@ -131,7 +135,7 @@ class VerifyRound:
         self.logits = torch.empty(rows, V, dtype=model.dtype, device=dev)
         self.out_tokens = torch.zeros(max_batch, R, **i32)
         self.out_len = torch.zeros(max_batch, **i32)
-        self.committed = torch.zeros(max_batch, **i32)
+        self.committed = self.report_dev[1]
         self.cu = {b: torch.arange(0, b * R + 1, R, **i32) for b in self.buckets}
         if method == "hybrid":
             self.ng_drafts = torch.zeros(max_batch, K, **i32)
@@ -154,8 +158,6 @@ class VerifyRound:
             self.uniforms = torch.zeros(max_batch, max(K, 1), dtype=torch.float32, device=dev)
             per_seq = (V,) if method == "model" else (R, V)  # model drafts only: one multinomial per sequence
             self.accept_noise = torch.ones(max_batch, *per_seq, dtype=model.dtype, device=dev)
-        # report rows: active flags, tokens committed, tokens drafted, drafts from the model
-        self.report_dev = torch.zeros(4, max_batch, **i32)
         self.report = torch.zeros(4, max_batch, dtype=torch.int32, pin_memory=True)
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
 
@@ -245,11 +247,7 @@ class VerifyRound:
         commit(self.out_tokens[:B], self.out_len[:B], self.num_drafts[:B], self.history[:B], self.hist_len[:B],
                self.prompt_len[:B], self.max_tokens[:B], self.max_len[:B], self.ignore_eos[:B], self.eos,
                self.active[:B], self.committed[:B], K)
-        # the round's report, copied to the host by the caller in one transfer
-        self.report_dev[0, :B].copy_(self.active[:B])
-        self.report_dev[1, :B].copy_(self.committed[:B])
-        self.report_dev[2, :B].copy_(self.num_drafts[:B])
-        self.report_dev[3, :B].copy_(self.draft_mode[:B])
+        # (the report rows are the state itself: the caller copies report_dev to the host)
 
     def capture(self) -> None:
         """Capture one graph per bucket (largest first, each in its own
