@@ -254,6 +254,16 @@ int nsv_commit(const int32_t* tokens, const int32_t* num_tokens,
  *   78-86 + layers/attention.py:71-112.
  * nsv_silu_mul: out [T, I] = silu(gate_up[:, :I]) * gate_up[:, I:].
  *   Replaces layers/activation.py:17-19.
+ * nsv_embed_rms_norm: the forward's prologue: r = embed[ids[t]] (embed
+ *   [vocab, E] bf16; an id outside [0, vocab) reads row 0, as the
+ *   reference's single-GPU lookup does) written to
+ *   residual_out, out = rmsnorm(r) * weight, and, when rope_out is not NULL,
+ *   rope_out[t] = cos_sin[positions[t]] ([T, D] fp32; position < 0 takes
+ *   row 0, past max_pos the last row), the per-row rotary table the
+ *   epilogue takes with positions == NULL.  Replaces the embedding lookup
+ *   (layers/embedding_head.py:32-46), layer 0's input LayerNorm
+ *   (layers/layernorm.py:18-35) and the rotary cache lookup
+ *   (layers/rotary_embedding.py:78-80).
  */
 int nsv_rms_norm(const void* x, const void* residual, void* residual_out,
                  const void* weight, void* out, int T, int E, float eps,
@@ -265,6 +275,11 @@ int nsv_qk_norm_rope_store(const void* qkv, const void* q_norm_w,
                            void* k_cache, void* v_cache, int T, int H,
                            int Hkv, int D, float eps, void* stream);
 int nsv_silu_mul(const void* gate_up, void* out, int T, int I, void* stream);
+int nsv_embed_rms_norm(const int64_t* ids, const void* embed, int64_t vocab,
+                       const void* weight, float eps, void* residual_out,
+                       void* out, int T, int E, const int64_t* positions,
+                       const float* cos_sin, int max_pos, int D,
+                       float* rope_out, void* stream);
 
 /*
  * Few-row bf16 linear layer of the verify forward: y = h W^T for the

@@ -50,6 +50,9 @@ SIGNATURES: dict[str, tuple] = {
     "nsv_qk_norm_rope_store": (
         _c_int, [_c_vp] * 4 + [_c_int] + [_c_vp] * 5 + [_c_int] * 4 + [_c_f32, _c_vp]),
     "nsv_silu_mul": (_c_int, [_c_vp, _c_vp, _c_int, _c_int, _c_vp]),
+    "nsv_embed_rms_norm": (
+        _c_int, [_c_vp, _c_vp, _c_i64, _c_vp, _c_f32, _c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_vp, _c_int, _c_int,
+                 _c_vp, _c_vp]),
     "nsv_linear_workspace_size": (_c_size, [_c_int] * 3),
     "nsv_linear": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_f32, _c_vp, _c_vp, _c_vp, _c_vp] + [_c_int] * 4
                    + [_c_vp, _c_size, _c_vp]),

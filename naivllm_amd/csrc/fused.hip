@@ -61,6 +61,54 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_residual_kernel(
 }
 
 // ---------------------------------------------------------------------------
+// Forward prologue: r = embed[ids[t]] (the residual stream's first value,
+// written to residual_out), out = rmsnorm(r) * w (layer 0's input norm), and
+// the rotary table row of the row's position (position < 0 takes row 0) into
+// rope_out [T, D] for every layer's epilogue.  An id outside [0, V) reads
+// row 0, as the reference's lookup does on one GPU (the id times its in-range
+// mask, layers/embedding_head.py:49-55).  One workgroup per row.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kNormThreads) void embed_norm_kernel(
+    const int64_t* __restrict__ ids, const uint16_t* __restrict__ embed, int64_t V, const uint16_t* __restrict__ w,
+    uint16_t* __restrict__ residual_out, uint16_t* __restrict__ out, int E, float eps,
+    const int64_t* __restrict__ positions, const float* __restrict__ cos_sin, int max_pos, int D,
+    float* __restrict__ rope_out) {
+  __shared__ float red[kNormThreads / 64];
+  const int64_t row = blockIdx.x;
+  const int64_t id = ids[row];
+  const bool valid = id >= 0 && id < V;
+  const uint16_t* xr = embed + (valid ? id : 0) * E;
+  if (rope_out) {
+    int64_t pos = positions[row];
+    pos = pos < 0 ? 0 : (pos >= max_pos ? max_pos - 1 : pos);
+    for (int i = threadIdx.x; i < D; i += kNormThreads) rope_out[row * D + i] = cos_sin[pos * D + i];
+  }
+  float ss = 0.f;
+  float v[16];  // thread t holds elements t, t + 256, ... (E <= 16 * 256)
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int i = threadIdx.x + j * kNormThreads;
+    v[j] = i < E ? bf(xr[i]) : 0.f;
+    ss += v[j] * v[j];
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < kNormThreads / 64; ++i) tot += red[i];
+  const float inv = rsqrtf(tot / (float)E + eps);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int i = threadIdx.x + j * kNormThreads;
+    if (i < E) {
+      residual_out[row * E + i] = f32_to_bf16_bits(v[j]);
+      out[row * E + i] = f32_to_bf16_bits(v[j] * inv * bf(w[i]));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Pre-attention epilogue.  qkv [T, (H + 2*Hkv) * D]: one wave per (row,
 // head); lane l holds elements l and l + D/2 (exactly the NeoX rotation
 // pair), D/2 <= 64.  q heads: RMSNorm * q_w, rotate, write q_out [T, H, D].
@@ -150,6 +198,19 @@ int nsv_rms_norm(const void* x, const void* residual, void* residual_out, const 
   hipLaunchKernelGGL(rms_norm_residual_kernel, dim3(T), dim3(kNormThreads), 0, (hipStream_t)stream,
                      (const uint16_t*)x, (const uint16_t*)residual, (uint16_t*)residual_out, (const uint16_t*)weight,
                      (uint16_t*)out, E, eps);
+  return nsv_launch_status();
+}
+
+int nsv_embed_rms_norm(const int64_t* ids, const void* embed, int64_t vocab, const void* weight, float eps,
+                       void* residual_out, void* out, int T, int E, const int64_t* positions, const float* cos_sin,
+                       int max_pos, int D, float* rope_out, void* stream) {
+  if (T < 0 || E <= 0 || E > 16 * kNormThreads || vocab <= 0) return NSV_ERR_ARG;
+  if (T == 0) return NSV_OK;
+  if (!ids || !embed || !weight || !residual_out || !out) return NSV_ERR_ARG;
+  if (rope_out && (!positions || !cos_sin || max_pos <= 0 || D <= 0)) return NSV_ERR_ARG;
+  hipLaunchKernelGGL(embed_norm_kernel, dim3(T), dim3(kNormThreads), 0, (hipStream_t)stream, ids,
+                     (const uint16_t*)embed, (int64_t)vocab, (const uint16_t*)weight, (uint16_t*)residual_out,
+                     (uint16_t*)out, E, eps, positions, cos_sin, max_pos, D, rope_out);
   return nsv_launch_status();
 }
 

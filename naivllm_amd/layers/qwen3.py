@@ -80,6 +80,22 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float, out: torch.Tenso
     _lib.check(rc, "rms_norm")
 
 
+def embed_rms_norm(ids: torch.Tensor, embed: torch.Tensor, weight: torch.Tensor, eps: float, residual_out, out,
+                   positions: torch.Tensor | None = None, cos_sin: torch.Tensor | None = None,
+                   rope_out: torch.Tensor | None = None) -> None:
+    """The forward's prologue (nsv_embed_rms_norm): residual_out = embed[ids],
+    out = rmsnorm(residual_out) * weight, and rope_out [T, D] = cos_sin rows
+    at the (clamped) positions when given."""
+    ids = ids.to(torch.int64).contiguous()
+    T, E = residual_out.shape
+    D = cos_sin.shape[1] if cos_sin is not None else 0
+    rc = _lib.lib().nsv_embed_rms_norm(
+        ids.data_ptr(), embed.data_ptr(), embed.shape[0], weight.data_ptr(), eps, residual_out.data_ptr(),
+        out.data_ptr(), T, E, _lib.ptr(positions), _lib.ptr(cos_sin), cos_sin.shape[0] if cos_sin is not None else 0,
+        D, _lib.ptr(rope_out), _lib.stream_ptr(residual_out.device))
+    _lib.check(rc, "embed_rms_norm")
+
+
 def qk_norm_rope_store(qkv, q_norm_w, k_norm_w, cos_sin, positions, slot_mapping, q_out, k_cache, v_cache,
                        H: int, Hkv: int, D: int, eps: float) -> None:
     """The pre-attention epilogue (nsv_qk_norm_rope_store).  positions None:
@@ -193,14 +209,17 @@ class Qwen3Verify:
         T = input_ids.shape[0]
         block_m = max(16, 1 << (max_q_len - 1).bit_length())
         I = cfg.intermediate_size
-        x = F.embedding(input_ids, self.embed)
-        resid = torch.empty_like(x)  # the residual stream
-        h = torch.empty_like(x)
+        resid = torch.empty(T, E, dtype=self.dtype, device=self.device)  # the residual stream
+        h = torch.empty_like(resid)
         q = torch.empty(T, H, D, dtype=self.dtype, device=self.device)
         attn = lambda li: paged_attention_verify(  # noqa: E731
             q, self.k_caches[li], self.v_caches[li], block_tables, context_lens, cu_seqlens_q, positions,
             self.scale, H, Hkv, D, self.block_size, block_m, max_q_len=max_q_len)
-        rms_norm(x, self.layers[0]["ln1"], eps, h, residual_out=resid)
+        # embedding lookup, layer 0's input norm, and the rotary rows of the step's
+        # positions (gathered once for every layer, so that each layer's epilogue
+        # loads them without first loading the positions) in one launch
+        rope_rows = torch.empty(T, D, dtype=torch.float32, device=self.device)
+        embed_rms_norm(input_ids, self.embed, self.layers[0]["ln1"], eps, resid, h, positions, self.rope, rope_rows)
         if T <= fused_rows(E):
             # Every RMSNorm after layer 0's is the prologue of the projection
             # that consumes it and every residual add the epilogue of the
@@ -209,10 +228,6 @@ class Qwen3Verify:
             act = torch.empty(T, I, dtype=self.dtype, device=self.device)
             ss_o = torch.empty(E // 16, T, dtype=torch.float32, device=self.device)  # partial sums of resid^2
             ss_d = torch.empty(E // 16, T, dtype=torch.float32, device=self.device)
-            # the rotary rows of the step's positions, gathered once for every layer
-            # (position < 0 takes row 0, as the epilogue kernel does), so that each
-            # layer's epilogue loads them without first loading the positions
-            rope_rows = self.rope.index_select(0, positions.clamp(0, self.rope.shape[0] - 1))
             for li, L in enumerate(self.layers):
                 if li == 0:
                     linear(h, L["qkv"], qkv)
@@ -232,7 +247,7 @@ class Qwen3Verify:
                 if li > 0:
                     rms_norm(x, L["ln1"], eps, h, residual=resid, residual_out=resid)
                 qkv = F.linear(h, L["qkv"])
-                qk_norm_rope_store(qkv, L["q_norm"], L["k_norm"], self.rope, positions, slot_mapping, q,
+                qk_norm_rope_store(qkv, L["q_norm"], L["k_norm"], rope_rows, None, slot_mapping, q,
                                    self.k_caches[li], self.v_caches[li], H, Hkv, D, eps)
                 x = F.linear(attn(li).view(T, H * D), L["o"])
                 rms_norm(x, L["ln2"], eps, h, residual=resid, residual_out=resid)

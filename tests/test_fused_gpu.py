@@ -105,6 +105,33 @@ def test_qk_norm_rope_store(D):
     assert torch.equal(q2, q_out) and torch.equal(kc2, kc) and torch.equal(vc2, vc)
 
 
+@pytest.mark.parametrize("T,E", [(9, 1024), (72, 1024), (3, 4096)])
+def test_embed_rms_norm(T, E):
+    # the forward's prologue against F.embedding + the fp32 RMSNorm and the
+    # rotary cache lookup: the residual stream is the embedding row exactly,
+    # the rotary rows are copies; an id past the vocabulary reads row 0 (the
+    # reference's single-GPU lookup), a position -1 takes rotary row 0
+    print(f"case: embed_rms_norm T={T} E={E}", flush=True)
+    g = gen(T + E)
+    V, D = 500, 128
+    embed, w = randn(g, V, E), randn(g, E)
+    ids = torch.randint(0, V, (T,), generator=torch.Generator().manual_seed(T)).cuda()
+    ids[0] = V + 7
+    positions = torch.randint(0, 4096, (T,), generator=torch.Generator().manual_seed(E)).cuda()
+    positions[-1] = -1
+    cos_sin = qm.rope_cache(Qwen3Config(head_dim=D, max_position=4096), "cuda")
+    resid = torch.empty(T, E, dtype=torch.bfloat16, device="cuda")
+    h = torch.empty_like(resid)
+    rope = torch.empty(T, D, device="cuda")
+    qm.embed_rms_norm(ids, embed, w, 1e-6, resid, h, positions, cos_sin, rope)
+    x = F.embedding(torch.where(ids < V, ids, torch.zeros_like(ids)), embed)
+    assert torch.equal(resid, x)
+    xf = x.float()
+    want = xf / torch.sqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6) * w.float()
+    torch.testing.assert_close(h.float(), want, **BF16)
+    assert torch.equal(rope, cos_sin[positions.clamp(0, 4095)])
+
+
 @pytest.mark.parametrize("T,I", [(1, 512), (72, 3072), (3, 1000)])
 def test_silu_mul(T, I):
     print(f"case: silu_mul T={T} I={I}", flush=True)
