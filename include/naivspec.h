@@ -307,6 +307,11 @@ int nsv_embed_rms_norm(const int64_t* ids, const void* embed, int64_t vocab,
  * workspace serves every call on a stream); otherwise no workspace is used.
  */
 size_t nsv_linear_workspace_size(int M, int N, int K);
+/* Rows of ss_out a residual-epilogue call with these M, N, K (and an
+ * RMSNorm prologue or not) writes: one partial sum of r^2 per row for each
+ * 16-column tile, or each 8-column tile where few rows over few tiles take
+ * 8-column workgroups.  The consumer's nss_in. */
+int nsv_linear_ss_rows(int M, int N, int K, int has_norm);
 int nsv_linear(const void* x, const void* norm_w, const float* ss_in,
                int nss_in, float eps, const void* weight, void* y,
                void* resid, float* ss_out, int M, int N, int K,

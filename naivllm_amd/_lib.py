@@ -54,6 +54,7 @@ SIGNATURES: dict[str, tuple] = {
         _c_int, [_c_vp, _c_vp, _c_i64, _c_vp, _c_f32, _c_vp, _c_vp, _c_int, _c_int, _c_vp, _c_vp, _c_int, _c_int,
                  _c_vp, _c_vp]),
     "nsv_linear_workspace_size": (_c_size, [_c_int] * 3),
+    "nsv_linear_ss_rows": (_c_int, [_c_int] * 4),
     "nsv_linear": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_f32, _c_vp, _c_vp, _c_vp, _c_vp] + [_c_int] * 4
                    + [_c_vp, _c_size, _c_vp]),
     "nsv_commit": (

@@ -72,14 +72,19 @@ __device__ __forceinline__ float bfv(uint32_t word, int hi) { return __uint_as_f
 // CUs takes twice the chunk (half the round trips of a long reduction).
 constexpr int lin_kc(int MT, bool small) { return (MT <= 2 ? 128 : 64) / (small ? 2 : 1); }
 
-template <int MT, bool NORM, int EPI, bool SMALL>  // EPI 0: plain, 1: SwiGLU, 2: residual
+// BNV: output columns per workgroup, 16, or 8 (the upper 8 MFMA columns
+// zero) where few rows and few tiles leave most CUs idle: half the weight
+// rows per CU and twice the workgroups (o_proj and down at 9 rows: 64 -> 128
+// workgroups, 4.9 -> 4.5 and 5.6 -> 5.0 us alone).
+template <int MT, bool NORM, int EPI, bool SMALL, int BNV = kBN>  // EPI 0: plain, 1: SwiGLU, 2: residual
 __global__ __launch_bounds__(kLinThreads, SMALL ? 2 : 1) void linear_kernel(LinearArgs a) {
+  static_assert(BNV == kBN || (BNV == 8 && EPI != 1), "8-column tiles: plain and residual epilogues");
   constexpr int MP = MT * 16;
   constexpr int KC = lin_kc(MT, SMALL);   // reduction elements per wave chunk
   constexpr int LPR = KC / 8;             // lanes per row of a whole-row load (16 bytes each)
   constexpr int RPI = 64 / LPR;           // rows per load instruction
   constexpr int STR = KC + 8;             // staged row stride (bf16): 16-byte reads of 16 rows hit distinct banks
-  constexpr int WL = kBN / RPI;           // weight loads per lane and chunk
+  constexpr int WL = BNV / RPI;           // weight loads per lane and chunk (rows < BNV)
   constexpr int AL = MP / RPI;            // activation loads per lane and chunk
   constexpr int STAGE = kLinWaves * (kBN + MP) * STR * 2;  // staged chunks, bytes
   constexpr int RED = kLinWaves * MP * (kBN + 1) * 4;      // cross-wave partial products, bytes
@@ -103,7 +108,7 @@ __global__ __launch_bounds__(kLinThreads, SMALL ? 2 : 1) void linear_kernel(Line
   const int half = a.N >> 1;
   auto wrow = [&](int col) -> int64_t {
     if constexpr (EPI == 1) return col < 8 ? tile * 8 + col : half + tile * 8 + (col - 8);
-    else return (int64_t)tile * kBN + col;
+    else return (int64_t)tile * BNV + col;
   };
   // the reduction in chunks of KC elements, dealt round-robin to the
   // ks * 8 waves of the tile (worker u = 8 kz + w takes chunks u, u + 8 ks,
@@ -136,6 +141,9 @@ __global__ __launch_bounds__(kLinThreads, SMALL ? 2 : 1) void linear_kernel(Line
   };
 
   uint16_t* st = reinterpret_cast<uint16_t*>(smem) + w * (kBN + MP) * STR;  // [16 weight + MP activation rows][STR]
+  if constexpr (BNV < kBN)  // weight rows BNV..15 are never loaded: zero once
+    for (int i = lane; i < (kBN - BNV) * STR / 8; i += NSV_WAVE)
+      reinterpret_cast<u32x4*>(st + BNV * STR)[i] = u32x4{0u, 0u, 0u, 0u};
   f32x4 acc[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -305,10 +313,11 @@ __global__ __launch_bounds__(kLinThreads, SMALL ? 2 : 1) void linear_kernel(Line
     }
   } else {
     // item = (row, 4 columns)
-    const int m = tid >> 2, q = tid & 3;
+    constexpr int QPR = BNV / 4;  // items per row
+    const int m = tid / QPR, q = tid % QPR;
     float ss = 0.f;
-    if (tid < MP * 4 && m < M) {
-      const int64_t off = (int64_t)(row0 + m) * a.N + (int64_t)tile * kBN + 4 * q;
+    if (tid < MP * QPR && m < M) {
+      const int64_t off = (int64_t)(row0 + m) * a.N + (int64_t)tile * BNV + 4 * q;
       float v[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) v[e] = bf16_bits_to_f32(f32_to_bf16_bits(colsum(m, 4 * q + e)));
@@ -327,10 +336,10 @@ __global__ __launch_bounds__(kLinThreads, SMALL ? 2 : 1) void linear_kernel(Line
                      (uint32_t)f32_to_bf16_bits(v[2]) | ((uint32_t)f32_to_bf16_bits(v[3]) << 16));
     }
     if constexpr (EPI == 2) {
-      // the 4 threads of a row are lanes 4m' .. 4m'+3 of one wave: fixed-order butterfly
+      // the QPR threads of a row are adjacent lanes of one wave: fixed-order butterfly
       ss += __shfl_xor(ss, 1, NSV_WAVE);
-      ss += __shfl_xor(ss, 2, NSV_WAVE);
-      if (tid < MP * 4 && m < M && q == 0) a.ss_out[(int64_t)tile * a.M + row0 + m] = ss;
+      if constexpr (QPR == 4) ss += __shfl_xor(ss, 2, NSV_WAVE);
+      if (tid < MP * QPR && m < M && q == 0) a.ss_out[(int64_t)tile * a.M + row0 + m] = ss;
     }
   }
 }
@@ -355,6 +364,12 @@ int lin_device_cus() {
   return cached[dev];
 }
 
+// 8-column tiles: plain or residual epilogue without the RMSNorm prologue,
+// at most 16 rows, fewer than 128 16-column tiles (no split reduction then).
+bool linear_half_tiles(int M, int N, bool norm, int epi) {
+  return !norm && epi != 1 && M <= 16 && N / kBN < 128 && N % 8 == 0;
+}
+
 template <int MT, bool SMALL>
 int launch_linear_kc(const LinearArgs& a, bool norm, int epi, dim3 grid, hipStream_t s) {
 #define NSV_LIN(NORM, EPI) hipLaunchKernelGGL((linear_kernel<MT, NORM, EPI, SMALL>), grid, dim3(kLinThreads), 0, s, a)
@@ -373,6 +388,19 @@ int launch_linear_kc(const LinearArgs& a, bool norm, int epi, dim3 grid, hipStre
 
 template <int MT>
 int launch_linear(const LinearArgs& a, bool norm, int epi, dim3 grid, hipStream_t s) {
+  if constexpr (MT == 1) {
+    if (linear_half_tiles(a.M, a.N, norm, epi)) {
+      const dim3 g2(a.N / 8, grid.y, 1);
+      if ((int64_t)g2.x * g2.y > lin_device_cus()) {
+        if (epi == 0) hipLaunchKernelGGL((linear_kernel<1, false, 0, true, 8>), g2, dim3(kLinThreads), 0, s, a);
+        else hipLaunchKernelGGL((linear_kernel<1, false, 2, true, 8>), g2, dim3(kLinThreads), 0, s, a);
+      } else {
+        if (epi == 0) hipLaunchKernelGGL((linear_kernel<1, false, 0, false, 8>), g2, dim3(kLinThreads), 0, s, a);
+        else hipLaunchKernelGGL((linear_kernel<1, false, 2, false, 8>), g2, dim3(kLinThreads), 0, s, a);
+      }
+      return nsv_launch_status();
+    }
+  }
   if ((int64_t)grid.x * grid.y * grid.z > lin_device_cus()) return launch_linear_kc<MT, true>(a, norm, epi, grid, s);
   return launch_linear_kc<MT, false>(a, norm, epi, grid, s);
 }
@@ -400,6 +428,11 @@ size_t linear_ws_bytes(int M, int N, int K) {
 }  // namespace
 
 extern "C" {
+
+int nsv_linear_ss_rows(int M, int N, int K, int has_norm) {
+  if (M <= 0 || N <= 0 || K <= 0 || N % kBN) return 0;
+  return linear_half_tiles(M, N, has_norm != 0, 2) ? N / 8 : N / kBN;
+}
 
 size_t nsv_linear_workspace_size(int M, int N, int K) {
   if (M <= 0 || N <= 0 || K <= 0 || N % kBN) return 0;

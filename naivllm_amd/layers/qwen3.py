@@ -107,6 +107,12 @@ def qk_norm_rope_store(qkv, q_norm_w, k_norm_w, cos_sin, positions, slot_mapping
     _lib.check(rc, "qk_norm_rope_store")
 
 
+def ss_rows(M: int, N: int, K: int, has_norm: bool = False) -> int:
+    """Rows of partial sums of r^2 a residual-epilogue linear writes (one per
+    16- or 8-column tile of the output)."""
+    return int(_lib.lib().nsv_linear_ss_rows(M, N, K, int(has_norm)))
+
+
 def linear(x: torch.Tensor, weight: torch.Tensor, y: torch.Tensor | None = None, *,
            norm_w: torch.Tensor | None = None, ss_in: torch.Tensor | None = None, eps: float = 1e-6,
            swiglu: bool = False, resid: torch.Tensor | None = None, ss_out: torch.Tensor | None = None) -> None:
@@ -116,7 +122,7 @@ def linear(x: torch.Tensor, weight: torch.Tensor, y: torch.Tensor | None = None,
     stream and ss_in [n, M] the producer's partial sums of x^2), else x.
     swiglu: weight is [gate; up] and y = silu(gate) * up.  resid: instead of
     writing y, add the product into the residual stream resid [M, N] and
-    write the new partial sums of resid^2 to ss_out [N / 16, M]."""
+    write the new partial sums of resid^2 to ss_out [ss_rows(M, N, K), M]."""
     M, K = x.shape
     N = weight.shape[0]
     epi = 2 if resid is not None else (1 if swiglu else 0)
@@ -226,8 +232,9 @@ class Qwen3Verify:
             # projection that produces it: 6 launches per layer.
             qkv = torch.empty(T, (H + 2 * Hkv) * D, dtype=self.dtype, device=self.device)
             act = torch.empty(T, I, dtype=self.dtype, device=self.device)
-            ss_o = torch.empty(E // 16, T, dtype=torch.float32, device=self.device)  # partial sums of resid^2
-            ss_d = torch.empty(E // 16, T, dtype=torch.float32, device=self.device)
+            # partial sums of resid^2 from o_proj and down (their tiles' count)
+            ss_o = torch.empty(ss_rows(T, E, H * D), T, dtype=torch.float32, device=self.device)
+            ss_d = torch.empty(ss_rows(T, E, I), T, dtype=torch.float32, device=self.device)
             for li, L in enumerate(self.layers):
                 if li == 0:
                     linear(h, L["qkv"], qkv)

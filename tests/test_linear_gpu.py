@@ -102,20 +102,23 @@ def test_linear_residual(M, N, K):
     w = randn(g, N, K, scale=K ** -0.5)
     r0 = randn(g, M, N)
     r = r0.clone()
-    ss = torch.full((N // 16, M), float("nan"), device="cuda")
+    rows = qm.ss_rows(M, N, K)  # one per 16-column tile, or 8-column tile (9 x 1024 x 2048)
+    ss = torch.full((rows, M), float("nan"), device="cuda")
     qm.linear(x, w, resid=r, ss_out=ss)
     prod = (x.float() @ w.float().t()).to(torch.bfloat16)
     torch.testing.assert_close(r.float(), (prod.float() + r0.float()).to(torch.bfloat16).float(), **BF16)
-    torch.testing.assert_close(ss, partial_squares(r, N // 16), rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(ss, partial_squares(r, rows), rtol=1e-5, atol=1e-5)
 
 
-def test_linear_chain_matches_unfused_layer():
+@pytest.mark.parametrize("M", [9, 18])
+def test_linear_chain_matches_unfused_layer(M):
     # o_proj (residual epilogue) -> gate_up (RMSNorm prologue, SwiGLU) ->
     # down (residual epilogue) -> LM head (RMSNorm prologue): the fused
-    # chain of one decoder layer against the unfused bf16 sequence
-    print("case: linear chain vs unfused layer", flush=True)
+    # chain of one decoder layer against the unfused bf16 sequence (at 9
+    # rows o_proj and down take 8-column tiles and write twice the partials)
+    print(f"case: linear chain vs unfused layer M={M}", flush=True)
     g = gen(5)
-    M, E, I, V = 18, 1024, 3072, 4096
+    E, I, V = 1024, 3072, 4096
     o = randn(g, M, 2048)
     resid = randn(g, M, E)
     w_o = randn(g, E, 2048, scale=2048 ** -0.5)
@@ -126,8 +129,8 @@ def test_linear_chain_matches_unfused_layer():
     ln_f = (1.0 + 0.3 * torch.randn(E, generator=g, device="cuda")).to(torch.bfloat16)
 
     r = resid.clone()
-    ss_o = torch.empty(E // 16, M, device="cuda")
-    ss_d = torch.empty(E // 16, M, device="cuda")
+    ss_o = torch.empty(qm.ss_rows(M, E, 2048), M, device="cuda")
+    ss_d = torch.empty(qm.ss_rows(M, E, I), M, device="cuda")
     act = torch.empty(M, I, dtype=torch.bfloat16, device="cuda")
     logits = torch.empty(M, V, dtype=torch.bfloat16, device="cuda")
     qm.linear(o, w_o, resid=r, ss_out=ss_o)
@@ -166,7 +169,7 @@ def test_split_reduction_is_deterministic_and_reusable(M, N, K):
     outs = []
     for _ in range(2):
         r = r0.clone()
-        ss = torch.empty(N // 16, M, device="cuda")
+        ss = torch.empty(qm.ss_rows(M, N, K), M, device="cuda")
         qm.linear(x, w, resid=r, ss_out=ss)
         outs.append((r, ss))
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
