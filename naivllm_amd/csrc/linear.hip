@@ -75,7 +75,7 @@ constexpr int lin_kc(int MT, bool small) { return (MT <= 2 ? 128 : 64) / (small 
 // BNV: output columns per workgroup, 16, or 8 (the upper 8 MFMA columns
 // zero) where few rows and few tiles leave most CUs idle: half the weight
 // rows per CU and twice the workgroups (o_proj and down at 9 rows: 64 -> 128
-// workgroups, 4.9 -> 4.5 and 5.6 -> 5.0 us alone).
+// workgroups, 4.9 -> 4.5 and 5.6 -> 5.0 us alone; at 18 rows 0.2 us each).
 template <int MT, bool NORM, int EPI, bool SMALL, int BNV = kBN>  // EPI 0: plain, 1: SwiGLU, 2: residual
 __global__ __launch_bounds__(kLinThreads, SMALL ? 2 : 1) void linear_kernel(LinearArgs a) {
   static_assert(BNV == kBN || (BNV == 8 && EPI != 1), "8-column tiles: plain and residual epilogues");
@@ -365,9 +365,9 @@ int lin_device_cus() {
 }
 
 // 8-column tiles: plain or residual epilogue without the RMSNorm prologue,
-// at most 16 rows, fewer than 128 16-column tiles (no split reduction then).
+// at most 32 rows, fewer than 128 16-column tiles (no split reduction then).
 bool linear_half_tiles(int M, int N, bool norm, int epi) {
-  return !norm && epi != 1 && M <= 16 && N / kBN < 128 && N % 8 == 0;
+  return !norm && epi != 1 && M <= 31 && N / kBN < 128 && N % 8 == 0;
 }
 
 template <int MT, bool SMALL>
@@ -388,15 +388,15 @@ int launch_linear_kc(const LinearArgs& a, bool norm, int epi, dim3 grid, hipStre
 
 template <int MT>
 int launch_linear(const LinearArgs& a, bool norm, int epi, dim3 grid, hipStream_t s) {
-  if constexpr (MT == 1) {
+  if constexpr (MT <= 2) {
     if (linear_half_tiles(a.M, a.N, norm, epi)) {
       const dim3 g2(a.N / 8, grid.y, 1);
       if ((int64_t)g2.x * g2.y > lin_device_cus()) {
-        if (epi == 0) hipLaunchKernelGGL((linear_kernel<1, false, 0, true, 8>), g2, dim3(kLinThreads), 0, s, a);
-        else hipLaunchKernelGGL((linear_kernel<1, false, 2, true, 8>), g2, dim3(kLinThreads), 0, s, a);
+        if (epi == 0) hipLaunchKernelGGL((linear_kernel<MT, false, 0, true, 8>), g2, dim3(kLinThreads), 0, s, a);
+        else hipLaunchKernelGGL((linear_kernel<MT, false, 2, true, 8>), g2, dim3(kLinThreads), 0, s, a);
       } else {
-        if (epi == 0) hipLaunchKernelGGL((linear_kernel<1, false, 0, false, 8>), g2, dim3(kLinThreads), 0, s, a);
-        else hipLaunchKernelGGL((linear_kernel<1, false, 2, false, 8>), g2, dim3(kLinThreads), 0, s, a);
+        if (epi == 0) hipLaunchKernelGGL((linear_kernel<MT, false, 0, false, 8>), g2, dim3(kLinThreads), 0, s, a);
+        else hipLaunchKernelGGL((linear_kernel<MT, false, 2, false, 8>), g2, dim3(kLinThreads), 0, s, a);
       }
       return nsv_launch_status();
     }

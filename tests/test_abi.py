@@ -144,7 +144,8 @@ def test_linear_rejects_bad_arguments_before_launch():
     # residual partial sums: per 8-column tile at few rows over few tiles, else per 16-column tile
     assert h.nsv_linear_ss_rows(9, 1024, 2048, 0) == 128
     assert h.nsv_linear_ss_rows(9, 1024, 2048, 1) == 64
-    assert h.nsv_linear_ss_rows(18, 1024, 2048, 0) == 64
+    assert h.nsv_linear_ss_rows(18, 1024, 2048, 0) == 128
+    assert h.nsv_linear_ss_rows(36, 1024, 2048, 0) == 64
     assert h.nsv_linear_ss_rows(9, 4096, 1024, 0) == 256
     n = h.nsv_linear_workspace_size(72, 1024, 2048)
     assert n >= 64 * 4 * 80 * 16 * 4

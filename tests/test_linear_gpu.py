@@ -94,7 +94,8 @@ def test_linear_swiglu(M, I, K):
     torch.testing.assert_close(y.float(), want, **BF16)
 
 
-@pytest.mark.parametrize("M,N,K", [(9, 1024, 2048), (72, 1024, 3072), (100, 256, 512), (3, 4096, 4096)])
+@pytest.mark.parametrize("M,N,K", [(9, 1024, 2048), (18, 1024, 3072), (72, 1024, 3072), (100, 256, 512),
+                                   (3, 4096, 4096)])
 def test_linear_residual(M, N, K):
     print(f"case: linear residual M={M} N={N} K={K}", flush=True)
     g = gen(M * 7 + N * 3 + K)
@@ -114,7 +115,7 @@ def test_linear_residual(M, N, K):
 def test_linear_chain_matches_unfused_layer(M):
     # o_proj (residual epilogue) -> gate_up (RMSNorm prologue, SwiGLU) ->
     # down (residual epilogue) -> LM head (RMSNorm prologue): the fused
-    # chain of one decoder layer against the unfused bf16 sequence (at 9
+    # chain of one decoder layer against the unfused bf16 sequence (up to 31
     # rows o_proj and down take 8-column tiles and write twice the partials)
     print(f"case: linear chain vs unfused layer M={M}", flush=True)
     g = gen(5)
