@@ -668,7 +668,15 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
 // An NS-stage register pipeline keeps the next NS tiles' loads in flight.
 // The sequence's whole block-table row is fetched in the first round trip
 // (with the context length and query range), so no load waits on another.
-template <int MT, int DH, int NS, int NW>
+#ifndef NSV_KS_WROW
+#define NSV_KS_WROW 1
+#endif
+// WROW: K tiles arrive as whole 2*DH-byte rows (VCH lanes per key, KPI keys
+// per load) and are reshaped through a per-wave LDS tile (chunk X of key r
+// at slot X ^ (r % VCH)) into the operand layout; a CU ingests whole rows
+// several times faster than the operand order's 64 bytes from each of 16
+// keys (config 4 on MI355X: 369 -> 356 us per call).
+template <int MT, int DH, int NS, int NW, bool WROW = (NSV_KS_WROW != 0)>
 __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyArgs a) {
   constexpr int NT = NW * 64;
   constexpr int TK = 16;          // keys per wave tile
@@ -680,7 +688,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
   constexpr int VL = TK / KPI;    // V loads per lane per tile
   constexpr int VSTR = DH + 16;   // staged V row stride (bf16): an odd multiple of 32 bytes
   constexpr int RSTR = DH + 4;    // merge-region row stride (floats)
-  constexpr int STAGE = NW * TK * VSTR * 2;
+  constexpr int KSTAGE = WROW ? NW * TK * DH * 2 : 0;  // whole-row K tiles
+  constexpr int STAGE = NW * TK * VSTR * 2 + KSTAGE;
   constexpr int MTILE_BYTES = NW * 16 * RSTR * 4;
   constexpr int SMEM = STAGE > MTILE_BYTES ? STAGE : MTILE_BYTES;
 
@@ -776,13 +785,14 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
   const char* kbase = (const char*)a.k_cache + hk * DH * 2;
   const char* vbase = (const char*)a.v_cache + hk * DH * 2;
   uint16_t* vl = reinterpret_cast<uint16_t*>(smem) + w * TK * VSTR;
+  unsigned char* kl = smem + NW * TK * VSTR * 2 + (WROW ? w * TK * DH * 2 : 0);
   __syncthreads();  // block-table row visible
 
   const int ntiles = (ke - kb + TK - 1) / TK;
   const int niter = (ntiles + NW - 1) / NW;  // same trip count in every wave
 
   struct Tile {
-    u32x4 k[KS];  // K as the A operand of S^T
+    u32x4 k[KS];  // K as the A operand of S^T, or (WROW) whole rows like v
     u32x4 v[VL];  // V rows, coalesced: load j, lane -> (key j * KPI + lane / VCH, chunk lane % VCH)
     int n0;
     int nvalid;   // the tile's existing keys are exactly its first nvalid
@@ -804,7 +814,13 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
     const char* kp = kbase + page_off;
     const char* vp = vbase + page_off;
     const unsigned base_key = (unsigned)(T.n0 & bs_mask);
-    {
+    if constexpr (WROW) {
+#pragma unroll
+      for (int j = 0; j < KS; ++j) {  // 16 keys x VCH chunks = KS loads of 64 chunks
+        const int r = j * KPI + lane / VCH, ch = lane % VCH;
+        T.k[j] = load16(kp + (base_key + (r < nvalid ? r : 0)) * row_bytes + ch * 16);
+      }
+    } else {
       const unsigned off = (base_key + (c < nvalid ? c : 0)) * row_bytes + g4 * 16;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) T.k[ks] = load16(kp + off + ks * 64);
@@ -819,13 +835,29 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
 
   auto compute = [&](const Tile& T) {
     if (T.nvalid == 0) return;  // uniform: nothing of this tile exists
+    u32x4 kA[KS];
+    if constexpr (WROW) {
+      // row-order tile -> LDS (this wave's rows; its LDS ops complete in order) -> operand order:
+      // lane (g4, c) takes key c, chunk 4 ks + g4
+#pragma unroll
+      for (int j = 0; j < KS; ++j) {
+        const int r = j * KPI + lane / VCH, ch = lane % VCH;
+        *reinterpret_cast<u32x4*>(kl + r * (DH * 2) + ((ch ^ (r % VCH)) << 4)) = T.k[j];
+      }
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        kA[ks] = *reinterpret_cast<const u32x4*>(kl + c * (DH * 2) + (((ks * 4 + g4) ^ (c % VCH)) << 4));
+    } else {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) kA[ks] = T.k[ks];
+    }
     f32x4 sacc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       f32x4 sv = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
-        sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(T.k[ks]), qB[mt][ks], sv, 0, 0, 0);
+        sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kA[ks]), qB[mt][ks], sv, 0, 0, 0);
       sacc[mt] = sv;
     }
     // stage V (this wave's private LDS rows; a wave's LDS ops complete in order)
