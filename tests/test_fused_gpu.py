@@ -184,15 +184,16 @@ def dense_forward(model: Qwen3Verify, ids: torch.Tensor) -> torch.Tensor:
     return norm(x, model.norm) @ f(model.lm_head).t()
 
 
-@pytest.mark.parametrize("fused,bs", [(True, 16), (True, 32), (False, 16)])
-def test_forward_matches_dense_fp32(fused, bs, monkeypatch):
+@pytest.mark.parametrize("fused,bs,head_few", [(True, 16, False), (True, 32, True), (False, 16, False)])
+def test_forward_matches_dense_fp32(fused, bs, head_few, monkeypatch):
     # two sequences: a first chunk written into a fresh paged cache, then a
     # 9-row verify chunk reading it back, against a dense fp32 forward; both
-    # the fused few-row path and the hipBLASLt path of wider batches
-    # (32-key pages: the 9-row chunk runs the fused epilogue + attention kernel)
-    print(f"case: qwen3 verify forward vs dense fp32, fused={fused} block_size={bs}", flush=True)
+    # the fused few-row path and the hipBLASLt path of wider batches, 16- and
+    # 32-key pages, the LM head on hipBLASLt or on the few-row kernel
+    print(f"case: qwen3 verify forward vs dense fp32, fused={fused} block_size={bs} head_few={head_few}", flush=True)
     monkeypatch.setattr(qm, "FUSED_ROWS", 1 << 30 if fused else 0)
     monkeypatch.setattr(qm, "FUSED_ROWS_WIDE", 1 << 30 if fused else 0)
+    monkeypatch.setattr(qm, "LM_HEAD_ROWS", 1 << 30 if head_few else 0)
     cfg = Qwen3Config(vocab_size=2048, hidden_size=256, num_layers=2, num_heads=4, num_kv_heads=2, head_dim=64,
                       intermediate_size=512, max_position=4096)
     model = Qwen3Verify(cfg, "cuda", seed=3)
