@@ -45,6 +45,15 @@ constexpr int kMaxCounterPairs = 16384;
 #define NSV_MAX_STAGES 4  // deepest key-split pipeline
 #endif
 
+// Workgroup barrier that orders LDS accesses only: unlike __syncthreads() it
+// does not wait for the wave's outstanding global loads, so a load pipeline
+// issued before it stays in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Pipeline depth of the d-sliced bf16 kernel.  Its slices re-read the pair's
 // K through L1, whose fill rate bounds it, and deeper pipelines only add
 // pressure there: on MI355X at config 2, 2 stages take 20.6 us, 3 21.3 us,
@@ -700,6 +709,11 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
   __shared__ float row_l[MP];
   __shared__ float row_ms[MP];
   __shared__ int row_pos[MP];
+  // The workgroup's query rows, the B operand of S^T, shared by the 8 waves
+  // (held in registers they would take 4 KS VGPRs per m-tile from the K/V
+  // pipeline); chunk X of row m at slot X ^ (m % VCH), so the 16 rows a
+  // B-operand read touches fall in distinct banks.
+  __shared__ __attribute__((aligned(16))) unsigned char q_lds[MP * DH * 2];
 
   // ---- workgroup -> (pair, split); every split of a pair on one XCD
   const int wg = blockIdx.x;
@@ -736,7 +750,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
     if (j < a.max_blocks) pages[j] = pv[i];
   }
 
-  bf16x8 qB[MT][KS];
+  constexpr int QPASS = (MP * VCH + NT - 1) / NT;  // 16-byte query chunks per thread
+  u32x4 qt[QPASS];
   int qpos[MT];
   int qmin = 0x7fffffff;
   auto load_q = [&]() {
@@ -745,12 +760,26 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
       const int m = mt * 16 + c;
       const int g = m / a.QL, t = m - g * a.QL;
       const bool ok = (m < a.Mv) && (t < qlen);
+      qpos[mt] = (int)a.positions[ok ? q0 + t : 0];
+    }
+    // padded and missing rows read the sequence's first row (their scores are masked)
+#pragma unroll
+    for (int i = 0; i < QPASS; ++i) {
+      const int idx = tid + i * NT;
+      const int m = idx / VCH, ch = idx % VCH;
+      const int g = m / a.QL, t = m - g * a.QL;
+      const bool ok = (idx < MP * VCH) && (m < a.Mv) && (t < qlen);
       const int row = ok ? q0 + t : 0;
       const int gg = ok ? g : 0;
-      qpos[mt] = (int)a.positions[row];
-      const bf16_t* qrow = (const bf16_t*)a.q + ((int64_t)row * a.H + hk * a.G + gg) * DH;
+      qt[i] = load16((const bf16_t*)a.q + ((int64_t)row * a.H + hk * a.G + gg) * DH + ch * 8);
+    }
+  };
+  auto store_q = [&]() {
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) qB[mt][ks] = as_bf16x8(load16(qrow + ks * 32 + g4 * 8));
+    for (int i = 0; i < QPASS; ++i) {
+      const int idx = tid + i * NT;
+      const int m = idx / VCH, ch = idx % VCH;
+      if (idx < MP * VCH) *reinterpret_cast<u32x4*>(q_lds + m * (DH * 2) + ((ch ^ (m % VCH)) << 4)) = qt[i];
     }
   };
   auto finish_positions = [&]() {
@@ -857,7 +886,10 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
       f32x4 sv = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
-        sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kA[ks]), qB[mt][ks], sv, 0, 0, 0);
+        sv = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+            as_bf16x8(kA[ks]),
+            as_bf16x8(*reinterpret_cast<const u32x4*>(q_lds + (mt * 16 + c) * (DH * 2) + (((ks * 4 + g4) ^ (c % VCH)) << 4))),
+            sv, 0, 0, 0);
       sacc[mt] = sv;
     }
     // stage V (this wave's private LDS rows; a wave's LDS ops complete in order)
@@ -925,6 +957,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
   for (int s = 0; s < NS; ++s) issue(T[s], s);
   __builtin_amdgcn_sched_barrier(0);
   finish_positions();
+  store_q();
+  lds_barrier();  // query rows visible; the tile loads stay in flight
   for (int it = 0; it < niter; it += NS) {
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
@@ -1414,8 +1448,10 @@ void launch_bf16_dc(const VerifyArgs& a, dim3 grid, hipStream_t s) {
 // Pipeline depth of the key-split kernel: as many K/V tiles in flight per
 // wave as the 256 VGPRs of a two-waves-per-SIMD launch hold without
 // spilling.  The estimate (VGPRs = 20 + MT * (per query m-tile) + NS * (per
-// tile)) matches the compiler's counts for every instantiation to within a
-// few registers.
+// tile)) still counts 4 KS VGPRs per m-tile for the query operand, which now
+// lives in LDS: that share is headroom (no instantiation spills), and the
+// third stage it would buy at three m-tiles measured slower on MI355X
+// (config 4: 332 vs 325 us per call).
 constexpr int ks_stages(int MT, int DH) {
   const int KS = DH / 32, DT = DH / 16, VL = 16 / (64 / (DH / 8));
   const int fixed = 20 + MT * (KS * 4 + DT * 4 + 8);
