@@ -125,6 +125,18 @@ def test_ragged_pad_rows_holes_and_empty_sequences(dtype):
     assert torch.all(out[torch.from_numpy(pad).cuda()] == 0)
 
 
+@pytest.mark.parametrize("num_heads", [2, 4, 8])
+def test_key_split_head_dim_64(num_heads):
+    # head_dim 64 through the key-split kernel (a fixed split length selects
+    # it): GQA groups 1, 2 and 4 over 2 kv heads give 1, 2 and 3 query
+    # m-tiles; a 64-dim row is 8 chunks of the LDS swizzle, not 16
+    print(f"case: key-split head_dim=64 H={num_heads} Hkv=2", flush=True)
+    vb = synth.verify_batch(29, [517, 33, 260], [9, 4, 9], num_heads=num_heads, num_kv_heads=2, head_dim=64,
+                            block_size=32, dtype="bf16")
+    out = _gpu(vb, max_q_len=9, kv_split_tokens=128)
+    assert_close(out, _oracle(vb), "bf16", f"ks d64 H{num_heads}")
+
+
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
 @pytest.mark.parametrize("bs", [4, 16])
 def test_small_pages(dtype, bs):
