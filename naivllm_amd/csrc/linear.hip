@@ -75,19 +75,23 @@ constexpr int lin_kc(int MT, bool small) { return (MT <= 2 ? 128 : 64) / (small 
 // BNV: output columns per workgroup, 16, or 8 (the upper 8 MFMA columns
 // zero) where few rows and few tiles leave most CUs idle: half the weight
 // rows per CU and twice the workgroups (o_proj and down at 9 rows: 64 -> 128
-// workgroups, 4.9 -> 4.5 and 5.6 -> 5.0 us alone; at 18 rows 0.2 us each).
+// workgroups, 4.9 -> 4.5 and 5.6 -> 5.0 us alone; at 18 rows 0.2 us each),
+// or 32 (two 16-column MFMA tiles per wave) for wide SwiGLU projections.
 template <int MT, bool NORM, int EPI, bool SMALL, int BNV = kBN>  // EPI 0: plain, 1: SwiGLU, 2: residual
 __global__ __launch_bounds__(kLinThreads, SMALL ? 2 : 1) void linear_kernel(LinearArgs a) {
-  static_assert(BNV == kBN || (BNV == 8 && EPI != 1), "8-column tiles: plain and residual epilogues");
+  static_assert(BNV == kBN || (BNV == 8 && EPI != 1) || (BNV == 32 && EPI == 1),
+                "8-column tiles: plain and residual epilogues; 32-column tiles: SwiGLU");
   constexpr int MP = MT * 16;
+  constexpr int WR = BNV > kBN ? BNV : kBN;  // staged weight rows (MFMA columns), BNV rounded up to 16
+  constexpr int NTL = WR / 16;               // 16-column MFMA tiles per workgroup
   constexpr int KC = lin_kc(MT, SMALL);   // reduction elements per wave chunk
   constexpr int LPR = KC / 8;             // lanes per row of a whole-row load (16 bytes each)
   constexpr int RPI = 64 / LPR;           // rows per load instruction
   constexpr int STR = KC + 8;             // staged row stride (bf16): 16-byte reads of 16 rows hit distinct banks
   constexpr int WL = BNV / RPI;           // weight loads per lane and chunk (rows < BNV)
   constexpr int AL = MP / RPI;            // activation loads per lane and chunk
-  constexpr int STAGE = kLinWaves * (kBN + MP) * STR * 2;  // staged chunks, bytes
-  constexpr int RED = kLinWaves * MP * (kBN + 1) * 4;      // cross-wave partial products, bytes
+  constexpr int STAGE = kLinWaves * (WR + MP) * STR * 2;  // staged chunks, bytes
+  constexpr int RED = kLinWaves * MP * (WR + 1) * 4;      // cross-wave partial products, bytes
   constexpr int SMEM = STAGE > RED ? STAGE : RED;
   __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM];
   __shared__ float inv_s[MP];
@@ -107,7 +111,8 @@ __global__ __launch_bounds__(kLinThreads, SMALL ? 2 : 1) void linear_kernel(Line
   // weight row of tile column col
   const int half = a.N >> 1;
   auto wrow = [&](int col) -> int64_t {
-    if constexpr (EPI == 1) return col < 8 ? tile * 8 + col : half + tile * 8 + (col - 8);
+    constexpr int GC = BNV / 2;  // SwiGLU: gate rows, then the matching up rows
+    if constexpr (EPI == 1) return col < GC ? tile * GC + col : half + tile * GC + (col - GC);
     else return (int64_t)tile * BNV + col;
   };
   // the reduction in chunks of KC elements, dealt round-robin to the
@@ -140,13 +145,15 @@ __global__ __launch_bounds__(kLinThreads, SMALL ? 2 : 1) void linear_kernel(Line
     ch.k0 = k0;
   };
 
-  uint16_t* st = reinterpret_cast<uint16_t*>(smem) + w * (kBN + MP) * STR;  // [16 weight + MP activation rows][STR]
+  uint16_t* st = reinterpret_cast<uint16_t*>(smem) + w * (WR + MP) * STR;  // [WR weight + MP activation rows][STR]
   if constexpr (BNV < kBN)  // weight rows BNV..15 are never loaded: zero once
     for (int i = lane; i < (kBN - BNV) * STR / 8; i += NSV_WAVE)
       reinterpret_cast<u32x4*>(st + BNV * STR)[i] = u32x4{0u, 0u, 0u, 0u};
-  f32x4 acc[MT];
+  f32x4 acc[NTL][MT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int nt = 0; nt < NTL; ++nt)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[nt][mt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   auto compute = [&](const Chunk& ch) {
     // stage the chunk's rows (this wave's LDS rows; a wave's LDS ops complete
@@ -167,17 +174,22 @@ __global__ __launch_bounds__(kLinThreads, SMALL ? 2 : 1) void linear_kernel(Line
 #pragma unroll
     for (int j = 0; j < AL; ++j) {
       const int m = rr + RPI * j;
-      *reinterpret_cast<u32x4*>(st + (kBN + m) * STR + cc * 8) = m < M ? ch.xv[j] : zero4;
+      *reinterpret_cast<u32x4*>(st + (WR + m) * STR + cc * 8) = m < M ? ch.xv[j] : zero4;
     }
     __builtin_amdgcn_wave_barrier();
     // operand reads: lane (g4, c) takes row c, elements 32 s + 8 g4 .. +7
 #pragma unroll
     for (int s = 0; s < KC / 32; ++s) {
-      const u32x4 bw = *reinterpret_cast<const u32x4*>(st + c * STR + 32 * s + 8 * g4);
+      u32x4 bw[NTL];
+#pragma unroll
+      for (int nt = 0; nt < NTL; ++nt)
+        bw[nt] = *reinterpret_cast<const u32x4*>(st + (nt * 16 + c) * STR + 32 * s + 8 * g4);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const u32x4 av = *reinterpret_cast<const u32x4*>(st + (kBN + mt * 16 + c) * STR + 32 * s + 8 * g4);
-        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(to_bf16x8(av), to_bf16x8(bw), acc[mt], 0, 0, 0);
+        const u32x4 av = *reinterpret_cast<const u32x4*>(st + (WR + mt * 16 + c) * STR + 32 * s + 8 * g4);
+#pragma unroll
+        for (int nt = 0; nt < NTL; ++nt)
+          acc[nt][mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(to_bf16x8(av), to_bf16x8(bw[nt]), acc[nt][mt], 0, 0, 0);
       }
     }
     __builtin_amdgcn_wave_barrier();
@@ -226,13 +238,15 @@ __global__ __launch_bounds__(kLinThreads, SMALL ? 2 : 1) void linear_kernel(Line
 
   // ---- sum the waves' partial products: lane (g4, c) holds C[16mt + 4g4 + i][c]
   __syncthreads();  // every wave is done with its staged weights (red aliases them)
-  float* red = reinterpret_cast<float*>(smem);  // [kLinWaves][MP][kBN + 1]
+  float* red = reinterpret_cast<float*>(smem);  // [kLinWaves][MP][WR + 1]
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+  for (int nt = 0; nt < NTL; ++nt)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) red[(w * MP + mt * 16 + g4 * 4 + i) * (kBN + 1) + c] = acc[mt][i];
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[(w * MP + mt * 16 + g4 * 4 + i) * (WR + 1) + nt * 16 + c] = acc[nt][mt][i];
   __syncthreads();
-  if (a.ks > 1) {
+  if (WR == kBN && a.ks > 1) {  // split reductions run on 16-column tiles only
     // ---- split-K: publish this workgroup's tile partial; the tile's last
     // workgroup to finish sums the ks partials in order (deterministic) and
     // runs the epilogue.  Partials and the arrival counter are agent-scope
@@ -287,13 +301,14 @@ __global__ __launch_bounds__(kLinThreads, SMALL ? 2 : 1) void linear_kernel(Line
   auto colsum = [&](int m, int col) {
     float v = 0.f;
 #pragma unroll
-    for (int ww = 0; ww < kLinWaves; ++ww) v += red[(ww * MP + m) * (kBN + 1) + col];
+    for (int ww = 0; ww < kLinWaves; ++ww) v += red[(ww * MP + m) * (WR + 1) + col];
     return NORM ? v * inv_s[m] : v;
   };
   if constexpr (EPI == 1) {
     // item = (row, 4 gate columns): silu(gate) * up for 4 outputs
-    if (tid < MP * 2) {
-      const int m = tid >> 1, q = tid & 1;
+    constexpr int GC = BNV / 2, QG = GC / 4;  // gate columns, items per row
+    if (tid < MP * QG) {
+      const int m = tid / QG, q = tid % QG;
       if (m < M) {
         uint32_t o[2];
 #pragma unroll
@@ -303,12 +318,12 @@ __global__ __launch_bounds__(kLinThreads, SMALL ? 2 : 1) void linear_kernel(Line
           for (int e = 0; e < 2; ++e) {
             const int col = 4 * q + 2 * j + e;
             const float g = bf16_bits_to_f32(f32_to_bf16_bits(colsum(m, col)));
-            const float u = bf16_bits_to_f32(f32_to_bf16_bits(colsum(m, 8 + col)));
+            const float u = bf16_bits_to_f32(f32_to_bf16_bits(colsum(m, GC + col)));
             r2[e] = g / (1.f + __expf(-g)) * u;
           }
           o[j] = (uint32_t)f32_to_bf16_bits(r2[0]) | ((uint32_t)f32_to_bf16_bits(r2[1]) << 16);
         }
-        *reinterpret_cast<uint2*>(a.y + (int64_t)(row0 + m) * half + tile * 8 + 4 * q) = make_uint2(o[0], o[1]);
+        *reinterpret_cast<uint2*>(a.y + (int64_t)(row0 + m) * half + tile * GC + 4 * q) = make_uint2(o[0], o[1]);
       }
     }
   } else {
@@ -386,8 +401,30 @@ int launch_linear_kc(const LinearArgs& a, bool norm, int epi, dim3 grid, hipStre
   return nsv_launch_status();
 }
 
+// 32-column tiles (16 gate + 16 up rows, one workgroup per CU) for the
+// SwiGLU epilogue where the 16-column grid would need two workgroups per CU:
+// each wave multiplies every staged activation chunk into two weight tiles
+// and the chunk is twice as long (whole 128-byte rows at 33-80 rows instead
+// of 64-byte ones), so a CU ingests ~40% fewer bytes per output column.
+// Measured on MI355X (gate_up alone, graph-replayed, rotating weights):
+// 0.6B (6144 x 1024, 192 workgroups) 7.45 -> 6.87 us at 9 rows, 11.31 ->
+// 10.09 us at 72; 8B (24576 x 4096, 768 workgroups) 51.3 -> 50.0 us at 18
+// rows, 107.4 -> 69.6 us at 72, but 43.9 -> 45.1 us at 9 rows, where the
+// two-per-CU 16-column grid keeps more loads in flight -- hence the row
+// bound once the wide grid exceeds one round.
+bool linear_wide_tiles(int M, int N, int epi) {
+  const int cus = lin_device_cus();
+  return epi == 1 && N % 32 == 0 && N / kBN > cus && (N / 32 <= cus || M > 16);
+}
+
 template <int MT>
 int launch_linear(const LinearArgs& a, bool norm, int epi, dim3 grid, hipStream_t s) {
+  if (linear_wide_tiles(a.M, a.N, epi)) {
+    const dim3 g2(a.N / 32, grid.y, 1);
+    if (norm) hipLaunchKernelGGL((linear_kernel<MT, true, 1, false, 32>), g2, dim3(kLinThreads), 0, s, a);
+    else hipLaunchKernelGGL((linear_kernel<MT, false, 1, false, 32>), g2, dim3(kLinThreads), 0, s, a);
+    return nsv_launch_status();
+  }
   if constexpr (MT <= 2) {
     if (linear_half_tiles(a.M, a.N, norm, epi)) {
       const dim3 g2(a.N / 8, grid.y, 1);

@@ -80,16 +80,26 @@ def test_linear_plain(M, N, K, norm):
         torch.testing.assert_close(y.float(), x.float() @ w.float().t(), **BF16)
 
 
-@pytest.mark.parametrize("M,I,K", [(9, 3072, 1024), (72, 3072, 1024), (5, 128, 256), (90, 256, 512), (40, 256, 1024)])
-def test_linear_swiglu(M, I, K):
-    print(f"case: linear swiglu M={M} I={I} K={K}", flush=True)
+# I >= 2080 puts more than 256 16-column tiles on the grid, which takes the
+# 32-column tiles (16 gate + 16 up rows) on up to 256 of them, or beyond 16
+# rows; (9, 12288, 4096) keeps the 16-column tiles; 90 rows take two row blocks
+@pytest.mark.parametrize("M,I,K,norm", [(9, 3072, 1024, True), (72, 3072, 1024, True), (5, 128, 256, True),
+                                        (90, 256, 512, True), (40, 256, 1024, True), (18, 3072, 1024, True),
+                                        (36, 3072, 1024, False), (50, 3072, 1024, True), (90, 3072, 1024, True),
+                                        (1, 3072, 1024, False), (9, 12288, 4096, True), (20, 12288, 4096, True)])
+def test_linear_swiglu(M, I, K, norm):
+    print(f"case: linear swiglu M={M} I={I} K={K} norm={norm}", flush=True)
     g = gen(M + I + K)
     r = randn(g, M, K)
     w = randn(g, 2 * I, K, scale=K ** -0.5)
-    nw = (1.0 + 0.3 * torch.randn(K, generator=g, device="cuda")).to(torch.bfloat16)
     y = torch.empty(M, I, dtype=torch.bfloat16, device="cuda")
-    qm.linear(r, w, y, norm_w=nw, ss_in=partial_squares(r, 4), eps=1e-6, swiglu=True)
-    gu = norm_linear_ref(r, nw, w, 1e-6).to(torch.bfloat16).float()  # the bf16 gate_up tensor
+    if norm:
+        nw = (1.0 + 0.3 * torch.randn(K, generator=g, device="cuda")).to(torch.bfloat16)
+        qm.linear(r, w, y, norm_w=nw, ss_in=partial_squares(r, 4), eps=1e-6, swiglu=True)
+        gu = norm_linear_ref(r, nw, w, 1e-6).to(torch.bfloat16).float()  # the bf16 gate_up tensor
+    else:
+        qm.linear(r, w, y, swiglu=True)
+        gu = (r.float() @ w.float().t()).to(torch.bfloat16).float()
     want = F.silu(gu[:, :I]) * gu[:, I:]
     torch.testing.assert_close(y.float(), want, **BF16)
 
