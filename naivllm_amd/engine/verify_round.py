@@ -278,6 +278,8 @@ class VerifyRound:
             g.replay()
         else:
             self.body(B)
-        self.report[:, :B].copy_(self.report_dev[:, :B], non_blocking=True)
+        # the whole [4, max_batch] block: one contiguous transfer (a column slice
+        # would first be gathered by a device copy kernel)
+        self.report.copy_(self.report_dev, non_blocking=True)
         torch.cuda.current_stream(self.model.device).synchronize()
         return self.report[:, :B]
