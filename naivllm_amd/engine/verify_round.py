@@ -158,7 +158,10 @@ class VerifyRound:
             self.uniforms = torch.zeros(max_batch, max(K, 1), dtype=torch.float32, device=dev)
             per_seq = (V,) if method == "model" else (R, V)  # model drafts only: one multinomial per sequence
             self.accept_noise = torch.ones(max_batch, *per_seq, dtype=model.dtype, device=dev)
-        self.report = torch.zeros(4, max_batch, dtype=torch.int32, pin_memory=True)
+        # two host copies of the report, so that one round's report can be read
+        # while the next round runs (launch / collect)
+        self.reports = [torch.zeros(4, max_batch, dtype=torch.int32, pin_memory=True) for _ in range(2)]
+        self.report_ready = [torch.cuda.Event() for _ in range(2)]
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
 
     def bucket_for(self, n: int) -> int:
@@ -269,10 +272,9 @@ class VerifyRound:
         torch.cuda.synchronize(self.model.device)
         self.active.copy_(saved)
 
-    def run(self, B: int) -> torch.Tensor:
-        """One round over slots 0..B-1 (B a bucket); returns the host report
-        [4, B]: active flags, tokens committed, tokens drafted, model-draft
-        flags."""
+    def launch(self, B: int, slot: int = 0) -> None:
+        """Enqueue one round over slots 0..B-1 (B a bucket) and the copy of
+        its report into host buffer `slot` (0 or 1); returns at once."""
         g = self.graphs.get(B)
         if g is not None:
             g.replay()
@@ -280,6 +282,16 @@ class VerifyRound:
             self.body(B)
         # the whole [4, max_batch] block: one contiguous transfer (a column slice
         # would first be gathered by a device copy kernel)
-        self.report.copy_(self.report_dev, non_blocking=True)
-        torch.cuda.current_stream(self.model.device).synchronize()
-        return self.report[:, :B]
+        self.reports[slot].copy_(self.report_dev, non_blocking=True)
+        self.report_ready[slot].record(torch.cuda.current_stream(self.model.device))
+
+    def collect(self, B: int, slot: int = 0) -> torch.Tensor:
+        """Wait for the report launched into `slot`; returns it as [4, B]:
+        active flags, tokens committed, tokens drafted, model-draft flags."""
+        self.report_ready[slot].synchronize()
+        return self.reports[slot][:, :B]
+
+    def run(self, B: int) -> torch.Tensor:
+        """One round over slots 0..B-1, waited for; returns its report [4, B]."""
+        self.launch(B, 0)
+        return self.collect(B, 0)

@@ -179,25 +179,46 @@ class SpecLLMEngine:
         t_prefill = time.perf_counter()
 
         live = [i for i, s in enumerate(seqs) if int(r.active[i])]
+        # tokens each sequence may still commit (max_tokens and length caps);
+        # a round commits at most K + 1
+        left = {i: min(params[i].max_tokens - seqs[i].num_completion_tokens,
+                       (params[i].max_model_length or self.max_model_length) - seqs[i].num_tokens) for i in live}
         rounds = 0
         decode_tokens = 0
-        while live:
-            B = r.bucket_for(max(live) + 1)
-            rep = r.run(B)
-            rounds += 1
-            act, com, dr, mdl = rep[0].tolist(), rep[1].tolist(), rep[2].tolist(), rep[3].tolist()
-            self.spec_stats["rounds"] += 1
-            fallback = 0
-            for i in live:
-                if self.spec_method != "none" and dr[i] > 0:
-                    self.spec_stats["drafted_tokens"] += dr[i]
-                    self.spec_stats["accepted_tokens"] += com[i]
-                    fallback += mdl[i]
-                decode_tokens += com[i]
-            if self.spec_method == "hybrid" and fallback:
-                self.spec_stats["model_fallback_rounds"] += 1
-                self.spec_stats["model_fallback_seqs"] += fallback
-            live = [i for i in live if act[i]]
+        pending = None  # (bucket, report slot) of a launched round whose report is unread
+        slot = 0
+        while live or pending is not None:
+            # The next round is enqueued before the pending round's report is
+            # read when the pending round cannot end every sequence (one that
+            # ignores EOS has more than K + 1 tokens left), so the host's
+            # bookkeeping overlaps the device.  A sequence that ends in the
+            # pending round is inactive on the device by then, and the round
+            # launched over it skips it (the bucket may be one size too large
+            # for that round).
+            launch = bool(live) and (pending is None or any(params[i].ignore_eos and left[i] > K + 1 for i in live))
+            if launch:
+                B = r.bucket_for(max(live) + 1)
+                r.launch(B, slot)
+                cur = (B, slot)
+                slot ^= 1
+                rounds += 1
+            if pending is not None:
+                rep = r.collect(*pending)
+                act, com, dr, mdl = rep.tolist()
+                self.spec_stats["rounds"] += 1
+                fallback = 0
+                for i in live:
+                    if self.spec_method != "none" and dr[i] > 0:
+                        self.spec_stats["drafted_tokens"] += dr[i]
+                        self.spec_stats["accepted_tokens"] += com[i]
+                        fallback += mdl[i]
+                    decode_tokens += com[i]
+                    left[i] -= com[i]
+                if self.spec_method == "hybrid" and fallback:
+                    self.spec_stats["model_fallback_rounds"] += 1
+                    self.spec_stats["model_fallback_seqs"] += fallback
+                live = [i for i in live if act[i]]
+            pending = cur if launch else None
         torch.cuda.synchronize(self.device)
         t_end = time.perf_counter()
 

@@ -129,7 +129,13 @@ def test_greedy_spec_equals_plain_decode_and_graph_equals_eager(block_size):
         eng = SpecLLMEngine({**base, **extra})
         res = eng.generate(prompts, sp)
         out[name] = [o["token_ids"] for o in res["outputs"]]
-        print(name, res["metrics"]["rounds"], res["metrics"]["spec_decoding"], flush=True)
+        m = res["metrics"]
+        print(name, m["rounds"], m["spec_decoding"], flush=True)
+        # rounds are enqueued ahead of their reports: every launched round is
+        # read back and counted once, and the decode tokens are exactly the
+        # tokens after each sequence's prefill token
+        assert m["rounds"] == m["spec_decoding"]["rounds"]
+        assert m["decode_tokens"] == sum(len(t) for t in out[name]) - len(prompts)
         del eng
         torch.cuda.empty_cache()
     assert all(len(x) == 40 for x in out["spec"])
