@@ -401,26 +401,32 @@ int launch_linear_kc(const LinearArgs& a, bool norm, int epi, dim3 grid, hipStre
   return nsv_launch_status();
 }
 
-// 32-column tiles (16 gate + 16 up rows, one workgroup per CU) for the
-// SwiGLU epilogue where the 16-column grid would need two workgroups per CU:
-// each wave multiplies every staged activation chunk into two weight tiles
-// and the chunk is twice as long (whole 128-byte rows at 33-80 rows instead
-// of 64-byte ones), so a CU ingests ~40% fewer bytes per output column.
-// Measured on MI355X (gate_up alone, graph-replayed, rotating weights):
-// 0.6B (6144 x 1024, 192 workgroups) 7.45 -> 6.87 us at 9 rows, 11.31 ->
-// 10.09 us at 72; 8B (24576 x 4096, 768 workgroups) 51.3 -> 50.0 us at 18
-// rows, 107.4 -> 69.6 us at 72, but 43.9 -> 45.1 us at 9 rows, where the
-// two-per-CU 16-column grid keeps more loads in flight -- hence the row
-// bound once the wide grid exceeds one round.
-bool linear_wide_tiles(int M, int N, int epi) {
+// 32-column tiles (16 gate + 16 up rows) for the SwiGLU epilogue where the
+// 16-column grid would need two workgroups per CU: each wave multiplies
+// every staged activation chunk into two weight tiles, so a CU ingests
+// fewer activation bytes per output column.  A wide grid that fits the CUs
+// keeps the full chunk (one workgroup per CU, whole 128-byte rows at 33-80
+// rows); a larger one takes half chunks and two workgroups per CU up to 32
+// rows.  Measured on MI355X (gate_up alone, graph-replayed, rotating
+// weights; 16-column tiles -> 32-column): 0.6B (6144 x 1024, 192
+// workgroups) 7.41 -> 6.84 us at 9 rows, 11.26 -> 10.13 us at 72; 8B (24576
+// x 4096, 768 workgroups) 44.3 -> 38.3 us at 9 rows and 52.5 -> 48.1 at 18
+// (two per CU; one per CU: 45.3 and 50.3), 76.1 -> 56.2 at 36 and 107.8 ->
+// 69.3 at 72 (one per CU; two per CU: 57.6 and 81.4).
+bool linear_wide_tiles(int N, int epi) {
   const int cus = lin_device_cus();
-  return epi == 1 && N % 32 == 0 && N / kBN > cus && (N / 32 <= cus || M > 16);
+  return epi == 1 && N % 32 == 0 && N / kBN > cus;
 }
 
 template <int MT>
 int launch_linear(const LinearArgs& a, bool norm, int epi, dim3 grid, hipStream_t s) {
-  if (linear_wide_tiles(a.M, a.N, epi)) {
+  if (linear_wide_tiles(a.N, epi)) {
     const dim3 g2(a.N / 32, grid.y, 1);
+    if (a.M <= 32 && (int64_t)g2.x * g2.y > lin_device_cus()) {  // half chunks, two workgroups per CU
+      if (norm) hipLaunchKernelGGL((linear_kernel<MT, true, 1, true, 32>), g2, dim3(kLinThreads), 0, s, a);
+      else hipLaunchKernelGGL((linear_kernel<MT, false, 1, true, 32>), g2, dim3(kLinThreads), 0, s, a);
+      return nsv_launch_status();
+    }
     if (norm) hipLaunchKernelGGL((linear_kernel<MT, true, 1, false, 32>), g2, dim3(kLinThreads), 0, s, a);
     else hipLaunchKernelGGL((linear_kernel<MT, false, 1, false, 32>), g2, dim3(kLinThreads), 0, s, a);
     return nsv_launch_status();
