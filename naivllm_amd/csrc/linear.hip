@@ -199,6 +199,17 @@ __global__ __launch_bounds__(kLinThreads, SMALL ? 2 : 1) void linear_kernel(Line
   Chunk A, B;
   auto k_of = [&](int i) { return (worker + i * nworkers) * KC; };
   if (nchunk > 0) issue(A, k_of(0));  // the first chunk streams in during the prologue below
+  // residual epilogue: this thread's 4 residual elements do not depend on the
+  // product, so their load is issued now rather than after the reduction
+  // (one memory round trip less at the end; the tile's columns are read and
+  // rewritten by this workgroup only)
+  uint2 resid_pre = make_uint2(0u, 0u);
+  if constexpr (EPI == 2) {
+    constexpr int QPR = BNV / 4;
+    const int m = tid / QPR, q = tid % QPR;
+    if (tid < MP * QPR && m < M)
+      resid_pre = *reinterpret_cast<const uint2*>(a.resid + (int64_t)(row0 + m) * a.N + (int64_t)tile * BNV + 4 * q);
+  }
 
   // ---- RMSNorm prologue: 1 / rms per row from the producer's partial sums,
   // added in a fixed order (thread part p sums slots p, p + P, ...; row m
@@ -338,8 +349,7 @@ __global__ __launch_bounds__(kLinThreads, SMALL ? 2 : 1) void linear_kernel(Line
       for (int e = 0; e < 4; ++e) v[e] = bf16_bits_to_f32(f32_to_bf16_bits(colsum(m, 4 * q + e)));
       uint16_t* dst = EPI == 2 ? a.resid : a.y;
       if constexpr (EPI == 2) {
-        const uint2 rv = *reinterpret_cast<const uint2*>(a.resid + off);
-        const uint32_t rw[2] = {rv.x, rv.y};
+        const uint32_t rw[2] = {resid_pre.x, resid_pre.y};
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           v[e] = bf16_bits_to_f32(f32_to_bf16_bits(v[e] + bfv(rw[e >> 1], e & 1)));  // the residual stream is bf16
