@@ -119,23 +119,6 @@ def measured_traffic(workload_config: int):
     return None
 
 
-def config3_prompts(batch: int, seed: int = 3, prefix: int = 1200, span: int = 40, vocab: int = 151936):
-    """BASELINE config 3 prompts: a 1200-token document made of 40-token
-    spans that recur across it (span i at chapter positions i and 7i mod N,
-    after benchmarks/rag_bench.py:80-105), followed per request by the
-    first tokens of one span as the question, so an answer quoting the
-    document is n-gram draftable."""
-    nspans = 12
-    spans = [[int(x) for x in synth.randint(seed, 90 + i, span, 100, vocab)] for i in range(nspans)]
-    doc = []
-    i = 0
-    while len(doc) < prefix:
-        doc += spans[i % nspans] + spans[(i * 7) % nspans][: span // 4]
-        i += 1
-    doc = doc[:prefix]
-    return [doc + spans[(b * 5 + 1) % nspans][:6] for b in range(batch)]
-
-
 def e2e_round(batches=(1, 2, 4, 8), tokens: int = 48, K: int = 8) -> dict:
     """the whole greedy n-gram verification round of a
     random-init Qwen3-0.6B (28 layers, bf16) at batch 1/2/4/8, one hipGraph
@@ -151,7 +134,7 @@ def e2e_round(batches=(1, 2, 4, 8), tokens: int = 48, K: int = 8) -> dict:
     out = {}
     for b in batches:
         before = dict(eng.spec_stats)
-        res = eng.generate(config3_prompts(b), sp)
+        res = eng.generate(synth.config3_prompts(b), sp)
         m = res["metrics"]
         st = m["spec_decoding"]
         drafted = st["drafted_tokens"] - before["drafted_tokens"]
@@ -192,7 +175,7 @@ def e2e_cascade(batches=(1, 8), tokens: int = 48, K: int = 8) -> dict:
     out = {}
     for b in batches:
         before = dict(eng.spec_stats)
-        res = eng.generate(config3_prompts(b, seed=5), sp)
+        res = eng.generate(synth.config3_prompts(b, seed=5), sp)
         m = res["metrics"]
         st = m["spec_decoding"]
         out[f"b{b}"] = {

@@ -82,6 +82,20 @@ int nsv_verify_attention(void* out, const void* q, const void* k_cache,
                          int dtype, int kv_split_tokens, void* workspace,
                          size_t workspace_bytes, void* stream);
 
+/* The kernel nsv_verify_attention runs for these arguments on a device
+ * with `cus` compute units (cus <= 0: the current device) and the key
+ * splits per sequence it cuts (1: none).  Host-only query, launches
+ * nothing; no reference counterpart (it exposes this library's plan for
+ * tests and tuning).  Returns what nsv_verify_attention would return for
+ * the shape (0, or the rejection code). */
+#define NSV_ATTN_DSLICED 0   /* bf16, workgroup = (pair, head-dim slice) */
+#define NSV_ATTN_KEY_SPLIT 1 /* bf16, workgroup = (pair, key split)      */
+#define NSV_ATTN_F32 2       /* fp32, VALU dot products                  */
+int nsv_verify_attention_plan(int B, int H, int Hkv, int D, int block_size,
+                              int max_blocks, int max_q_len, int dtype,
+                              int kv_split_tokens, int cus, int* kernel,
+                              int* splits);
+
 /*
  * Paged KV scatter.
  * Replaces layers/attention.py:71-112 (store_kvcache) and its kernel :9-68:
@@ -312,6 +326,15 @@ size_t nsv_linear_workspace_size(int M, int N, int K);
  * 16-column tile, or each 8-column tile where few rows over few tiles take
  * 8-column workgroups.  The consumer's nss_in. */
 int nsv_linear_ss_rows(int M, int N, int K, int has_norm);
+/* The dispatch nsv_linear takes for these arguments on a device with `cus`
+ * compute units (cus <= 0: the current device): output columns per
+ * workgroup (8, 16 or 32), workgroups per 16-column tile that split the
+ * reduction (> 1 only with 16-column tiles), and whether half-size
+ * reduction chunks are used.  Host-only query, launches nothing; no
+ * reference counterpart (it exposes this library's tiling for tests and
+ * tuning). */
+int nsv_linear_plan(int M, int N, int K, int has_norm, int epilogue, int cus,
+                    int* tile_cols, int* splits, int* half_chunks);
 int nsv_linear(const void* x, const void* norm_w, const float* ss_in,
                int nss_in, float eps, const void* weight, void* y,
                void* resid, float* ss_out, int M, int N, int K,

@@ -29,6 +29,7 @@ SIGNATURES: dict[str, tuple] = {
     "nsv_error_string": (ctypes.c_char_p, [_c_int]),
     "nsv_verify_attention_workspace_size": (
         _c_size, [_c_int] * 9),
+    "nsv_verify_attention_plan": (_c_int, [_c_int] * 10 + [_c_vp] * 2),
     "nsv_verify_attention": (
         _c_int,
         [_c_vp] * 8 + [_c_f32] + [_c_int] * 10 + [_c_vp, _c_size, _c_vp]),
@@ -55,6 +56,7 @@ SIGNATURES: dict[str, tuple] = {
                  _c_vp, _c_vp]),
     "nsv_linear_workspace_size": (_c_size, [_c_int] * 3),
     "nsv_linear_ss_rows": (_c_int, [_c_int] * 4),
+    "nsv_linear_plan": (_c_int, [_c_int] * 6 + [_c_vp] * 3),
     "nsv_linear": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_f32, _c_vp, _c_vp, _c_vp, _c_vp] + [_c_int] * 4
                    + [_c_vp, _c_size, _c_vp]),
     "nsv_commit": (

@@ -72,13 +72,23 @@ __device__ __forceinline__ float bfv(uint32_t word, int hi) { return __uint_as_f
 // CUs takes twice the chunk (half the round trips of a long reduction).
 constexpr int lin_kc(int MT, bool small) { return (MT <= 2 ? 128 : 64) / (small ? 2 : 1); }
 
+// Minimum waves per SIMD the compiler must allow (HIP's second
+// __launch_bounds__ argument is amdgpu_waves_per_eu, not workgroups per
+// CU): two resident 8-wave workgroups are 4 waves per SIMD, i.e. at most
+// 128 VGPRs.  The 32-column SwiGLU tiles with half chunks need 150 VGPRs
+// from two row tiles on (224+ with full chunks); bounded to 128 they spill,
+// so they run one workgroup per CU and keep the half chunk for its shorter
+// staging round trips (8B gate_up at 18 rows: 48.1 us, against 50.3 with
+// full chunks and 52.5 with 16-column tiles).
+constexpr int lin_waves_per_eu(int MT, bool small, int bnv) { return small && !(bnv == 32 && MT >= 2) ? 4 : 1; }
+
 // BNV: output columns per workgroup, 16, or 8 (the upper 8 MFMA columns
 // zero) where few rows and few tiles leave most CUs idle: half the weight
 // rows per CU and twice the workgroups (o_proj and down at 9 rows: 64 -> 128
 // workgroups, 4.9 -> 4.5 and 5.6 -> 5.0 us alone; at 18 rows 0.2 us each),
 // or 32 (two 16-column MFMA tiles per wave) for wide SwiGLU projections.
 template <int MT, bool NORM, int EPI, bool SMALL, int BNV = kBN>  // EPI 0: plain, 1: SwiGLU, 2: residual
-__global__ __launch_bounds__(kLinThreads, SMALL ? 2 : 1) void linear_kernel(LinearArgs a) {
+__global__ __launch_bounds__(kLinThreads, lin_waves_per_eu(MT, SMALL, BNV)) void linear_kernel(LinearArgs a) {
   static_assert(BNV == kBN || (BNV == 8 && EPI != 1) || (BNV == 32 && EPI == 1),
                 "8-column tiles: plain and residual epilogues; 32-column tiles: SwiGLU");
   constexpr int MP = MT * 16;
@@ -390,25 +400,9 @@ int lin_device_cus() {
 }
 
 // 8-column tiles: plain or residual epilogue without the RMSNorm prologue,
-// at most 32 rows, fewer than 128 16-column tiles (no split reduction then).
+// at most 31 rows, fewer than 128 16-column tiles (no split reduction then).
 bool linear_half_tiles(int M, int N, bool norm, int epi) {
   return !norm && epi != 1 && M <= 31 && N / kBN < 128 && N % 8 == 0;
-}
-
-template <int MT, bool SMALL>
-int launch_linear_kc(const LinearArgs& a, bool norm, int epi, dim3 grid, hipStream_t s) {
-#define NSV_LIN(NORM, EPI) hipLaunchKernelGGL((linear_kernel<MT, NORM, EPI, SMALL>), grid, dim3(kLinThreads), 0, s, a)
-  if (norm) {
-    if (epi == 0) NSV_LIN(true, 0);
-    else if (epi == 1) NSV_LIN(true, 1);
-    else NSV_LIN(true, 2);
-  } else {
-    if (epi == 0) NSV_LIN(false, 0);
-    else if (epi == 1) NSV_LIN(false, 1);
-    else NSV_LIN(false, 2);
-  }
-#undef NSV_LIN
-  return nsv_launch_status();
 }
 
 // 32-column tiles (16 gate + 16 up rows) for the SwiGLU epilogue where the
@@ -416,46 +410,17 @@ int launch_linear_kc(const LinearArgs& a, bool norm, int epi, dim3 grid, hipStre
 // every staged activation chunk into two weight tiles, so a CU ingests
 // fewer activation bytes per output column.  A wide grid that fits the CUs
 // keeps the full chunk (one workgroup per CU, whole 128-byte rows at 33-80
-// rows); a larger one takes half chunks and two workgroups per CU up to 32
-// rows.  Measured on MI355X (gate_up alone, graph-replayed, rotating
-// weights; 16-column tiles -> 32-column): 0.6B (6144 x 1024, 192
-// workgroups) 7.41 -> 6.84 us at 9 rows, 11.26 -> 10.13 us at 72; 8B (24576
-// x 4096, 768 workgroups) 44.3 -> 38.3 us at 9 rows and 52.5 -> 48.1 at 18
-// (two per CU; one per CU: 45.3 and 50.3), 76.1 -> 56.2 at 36 and 107.8 ->
-// 69.3 at 72 (one per CU; two per CU: 57.6 and 81.4).
-bool linear_wide_tiles(int N, int epi) {
-  const int cus = lin_device_cus();
-  return epi == 1 && N % 32 == 0 && N / kBN > cus;
-}
-
-template <int MT>
-int launch_linear(const LinearArgs& a, bool norm, int epi, dim3 grid, hipStream_t s) {
-  if (linear_wide_tiles(a.N, epi)) {
-    const dim3 g2(a.N / 32, grid.y, 1);
-    if (a.M <= 32 && (int64_t)g2.x * g2.y > lin_device_cus()) {  // half chunks, two workgroups per CU
-      if (norm) hipLaunchKernelGGL((linear_kernel<MT, true, 1, true, 32>), g2, dim3(kLinThreads), 0, s, a);
-      else hipLaunchKernelGGL((linear_kernel<MT, false, 1, true, 32>), g2, dim3(kLinThreads), 0, s, a);
-      return nsv_launch_status();
-    }
-    if (norm) hipLaunchKernelGGL((linear_kernel<MT, true, 1, false, 32>), g2, dim3(kLinThreads), 0, s, a);
-    else hipLaunchKernelGGL((linear_kernel<MT, false, 1, false, 32>), g2, dim3(kLinThreads), 0, s, a);
-    return nsv_launch_status();
-  }
-  if constexpr (MT <= 2) {
-    if (linear_half_tiles(a.M, a.N, norm, epi)) {
-      const dim3 g2(a.N / 8, grid.y, 1);
-      if ((int64_t)g2.x * g2.y > lin_device_cus()) {
-        if (epi == 0) hipLaunchKernelGGL((linear_kernel<MT, false, 0, true, 8>), g2, dim3(kLinThreads), 0, s, a);
-        else hipLaunchKernelGGL((linear_kernel<MT, false, 2, true, 8>), g2, dim3(kLinThreads), 0, s, a);
-      } else {
-        if (epi == 0) hipLaunchKernelGGL((linear_kernel<MT, false, 0, false, 8>), g2, dim3(kLinThreads), 0, s, a);
-        else hipLaunchKernelGGL((linear_kernel<MT, false, 2, false, 8>), g2, dim3(kLinThreads), 0, s, a);
-      }
-      return nsv_launch_status();
-    }
-  }
-  if ((int64_t)grid.x * grid.y * grid.z > lin_device_cus()) return launch_linear_kc<MT, true>(a, norm, epi, grid, s);
-  return launch_linear_kc<MT, false>(a, norm, epi, grid, s);
+// rows); a larger one takes half chunks up to 32 rows (two workgroups per
+// CU at up to 16 rows, one beyond: see lin_waves_per_eu).  Measured on
+// MI355X (gate_up alone, graph-replayed, rotating weights; 16-column tiles
+// -> 32-column): 0.6B (6144 x 1024, 192 workgroups) 7.41 -> 6.84 us at 9
+// rows, 11.26 -> 10.13 us at 72; 8B (24576 x 4096, 768 workgroups) 44.3 ->
+// 38.3 us at 9 rows and 52.5 -> 48.1 at 18 (full chunks: 45.3 and 50.3),
+// 76.1 -> 56.2 at 36 and 107.8 -> 69.3 at 72 (full chunks; half chunks:
+// 57.6 and 81.4).  Only grids of >= 128 16-column tiles take them, where
+// the reduction is never split (linear_splits), whatever the CU count.
+bool linear_wide_tiles(int N, int epi, int cus) {
+  return epi == 1 && N % 32 == 0 && N / kBN > cus && N / kBN >= 128;
 }
 
 // Workgroups per 16-column tile: a split of the reduction when the tiles
@@ -471,11 +436,68 @@ int linear_splits(int M, int N, int K) {
   return ks;
 }
 
-size_t linear_ws_bytes(int M, int N, int K) {
+// The dispatch of one call: tile width first, then the split count, which
+// only the 16-column tiles take (the 8- and 32-column kernels deal the
+// reduction to one workgroup's 8 waves and never merge partials).
+struct LinPlan {
+  int cols;    // output columns per workgroup: 8, 16 or 32
+  int ks;      // workgroups per 16-column tile (split reduction), 1 otherwise
+  bool small;  // half chunks (and two workgroups per CU where registers allow)
+};
+
+LinPlan linear_plan(int M, int N, int K, bool norm, int epi, int cus) {
+  const int gy = (M + kMaxRows - 1) / kMaxRows;
+  if (linear_wide_tiles(N, epi, cus)) return {32, 1, M <= 32 && (int64_t)(N / 32) * gy > cus};
+  if (linear_half_tiles(M, N, norm, epi)) return {8, 1, (int64_t)(N / 8) * gy > cus};
   const int ks = linear_splits(M, N, K);
+  return {16, ks, (int64_t)(N / kBN) * gy * ks > cus};
+}
+
+size_t linear_ws_bytes(int ks, int N) {
   if (ks <= 1) return 0;
   const size_t tiles = (size_t)(N / kBN);
   return ((tiles * sizeof(unsigned) + 255) & ~(size_t)255) + tiles * ks * kMaxRows * kBN * sizeof(float);
+}
+
+template <int MT, int BNV, bool SMALL>
+int launch_linear_tiles(const LinearArgs& a, bool norm, int epi, dim3 grid, hipStream_t s) {
+#define NSV_LIN(NORM, EPI) \
+  hipLaunchKernelGGL((linear_kernel<MT, NORM, EPI, SMALL, BNV>), grid, dim3(kLinThreads), 0, s, a)
+  if constexpr (BNV == 32) {  // SwiGLU only
+    if (norm) NSV_LIN(true, 1);
+    else NSV_LIN(false, 1);
+  } else if constexpr (BNV == 8) {  // plain or residual, no prologue
+    if (epi == 0) NSV_LIN(false, 0);
+    else NSV_LIN(false, 2);
+  } else if (norm) {
+    if (epi == 0) NSV_LIN(true, 0);
+    else if (epi == 1) NSV_LIN(true, 1);
+    else NSV_LIN(true, 2);
+  } else {
+    if (epi == 0) NSV_LIN(false, 0);
+    else if (epi == 1) NSV_LIN(false, 1);
+    else NSV_LIN(false, 2);
+  }
+#undef NSV_LIN
+  return nsv_launch_status();
+}
+
+template <int MT>
+int launch_linear(const LinearArgs& a, const LinPlan& p, bool norm, int epi, hipStream_t s) {
+  const dim3 grid(a.N / p.cols, (a.M + kMaxRows - 1) / kMaxRows, p.ks);
+  if (p.cols == 32) {
+    return p.small ? launch_linear_tiles<MT, 32, true>(a, norm, epi, grid, s)
+                   : launch_linear_tiles<MT, 32, false>(a, norm, epi, grid, s);
+  }
+  if constexpr (MT <= 2) {  // 8-column tiles take at most 31 rows
+    if (p.cols == 8) {
+      return p.small ? launch_linear_tiles<MT, 8, true>(a, norm, epi, grid, s)
+                     : launch_linear_tiles<MT, 8, false>(a, norm, epi, grid, s);
+    }
+  }
+  if (p.cols != kBN) return NSV_ERR_UNSUPPORTED;
+  return p.small ? launch_linear_tiles<MT, kBN, true>(a, norm, epi, grid, s)
+                 : launch_linear_tiles<MT, kBN, false>(a, norm, epi, grid, s);
 }
 
 }  // namespace
@@ -489,7 +511,17 @@ int nsv_linear_ss_rows(int M, int N, int K, int has_norm) {
 
 size_t nsv_linear_workspace_size(int M, int N, int K) {
   if (M <= 0 || N <= 0 || K <= 0 || N % kBN) return 0;
-  return linear_ws_bytes(M, N, K);
+  return linear_ws_bytes(linear_splits(M, N, K), N);
+}
+
+int nsv_linear_plan(int M, int N, int K, int has_norm, int epilogue, int cus, int* tile_cols, int* splits,
+                    int* half_chunks) {
+  if (M <= 0 || N <= 0 || K <= 0 || epilogue < 0 || epilogue > 2 || N % kBN || K % 8) return NSV_ERR_ARG;
+  const LinPlan p = linear_plan(M, N, K, has_norm != 0, epilogue, cus > 0 ? cus : lin_device_cus());
+  if (tile_cols) *tile_cols = p.cols;
+  if (splits) *splits = p.ks;
+  if (half_chunks) *half_chunks = p.small ? 1 : 0;
+  return NSV_OK;
 }
 
 int nsv_linear(const void* x, const void* norm_w, const float* ss_in, int nss_in, float eps, const void* weight,
@@ -501,22 +533,21 @@ int nsv_linear(const void* x, const void* norm_w, const float* ss_in, int nss_in
   if (!x || !weight) return NSV_ERR_ARG;
   if (norm_w && (!ss_in || nss_in <= 0)) return NSV_ERR_ARG;
   if (epilogue == 2 ? (!resid || !ss_out) : !y) return NSV_ERR_ARG;
-  const int ks = linear_splits(M, N, K);
-  const size_t need = linear_ws_bytes(M, N, K);
+  const bool norm = norm_w != nullptr;
+  const LinPlan p = linear_plan(M, N, K, norm, epilogue, lin_device_cus());
+  const size_t need = linear_ws_bytes(p.ks, N);
   if (need && (!workspace || workspace_bytes < need)) return NSV_ERR_WORKSPACE;
   const size_t cnt = ((size_t)(N / kBN) * sizeof(unsigned) + 255) & ~(size_t)255;
   LinearArgs a{(const uint16_t*)x, (const uint16_t*)norm_w, ss_in, nss_in, eps, (const uint16_t*)weight,
-               (uint16_t*)y, (uint16_t*)resid, ss_out, M, N, K, ks,
+               (uint16_t*)y, (uint16_t*)resid, ss_out, M, N, K, p.ks,
                need ? (float*)((char*)workspace + cnt) : nullptr, need ? (unsigned*)workspace : nullptr};
-  const dim3 grid(N / kBN, (M + kMaxRows - 1) / kMaxRows, ks);
   hipStream_t s = (hipStream_t)stream;
-  const bool norm = norm_w != nullptr;
   switch ((min(M, kMaxRows) + 15) / 16) {
-    case 1: return launch_linear<1>(a, norm, epilogue, grid, s);
-    case 2: return launch_linear<2>(a, norm, epilogue, grid, s);
-    case 3: return launch_linear<3>(a, norm, epilogue, grid, s);
-    case 4: return launch_linear<4>(a, norm, epilogue, grid, s);
-    default: return launch_linear<5>(a, norm, epilogue, grid, s);
+    case 1: return launch_linear<1>(a, p, norm, epilogue, s);
+    case 2: return launch_linear<2>(a, p, norm, epilogue, s);
+    case 3: return launch_linear<3>(a, p, norm, epilogue, s);
+    case 4: return launch_linear<4>(a, p, norm, epilogue, s);
+    default: return launch_linear<5>(a, p, norm, epilogue, s);
   }
 }
 

@@ -1340,7 +1340,7 @@ int device_cus() {
 }
 
 int make_plan(int B, int H, int Hkv, int D, int block_size, int max_blocks, int max_q_len, int dtype,
-              int kv_split_tokens, Plan* p) {
+              int kv_split_tokens, int cus, Plan* p) {
   if (B < 0 || H <= 0 || Hkv <= 0 || max_blocks <= 0 || max_q_len <= 0) return NSV_ERR_ARG;
   if (dtype != NSV_F32 && dtype != NSV_BF16) return NSV_ERR_ARG;
   if (H % Hkv) return NSV_ERR_UNSUPPORTED;
@@ -1369,7 +1369,7 @@ int make_plan(int B, int H, int Hkv, int D, int block_size, int max_blocks, int 
   // are within 5% (d-sliced ahead); at 128 pairs x 16k-32k keys the
   // key-split kernel is 2x faster.  So key-split when the pairs fill the
   // chip without splits, or when a table holds >= 4096 keys.
-  const int64_t ks_slots = (int64_t)device_cus() * (8 / kKsWaves);  // resident workgroups
+  const int64_t ks_slots = (int64_t)cus * (8 / kKsWaves);  // resident workgroups
   const bool ks_fits = p->MT <= 3 && block_size >= 16 && max_blocks <= kMaxSplitPages &&
                        (pairs <= kMaxCounterPairs || (kv_split_tokens == 0 && pairs >= ks_slots));
   const bool ks_wins = kv_split_tokens > 0 || pairs >= ks_slots || max_ctx >= 4096;
@@ -1395,7 +1395,6 @@ int make_plan(int B, int H, int Hkv, int D, int block_size, int max_blocks, int 
     return NSV_OK;
   }
   if (dtype == NSV_BF16) {
-    const int cus = device_cus();
     // widest head-dim slice whose double-buffered K/V tiles and accumulators
     // fit the register file without spilling: 64 dims up to 32 padded query
     // rows, 32 beyond
@@ -1521,8 +1520,20 @@ const char* nsv_error_string(int code) {
 size_t nsv_verify_attention_workspace_size(int B, int H, int Hkv, int D, int block_size, int max_blocks,
                                            int max_q_len, int dtype, int kv_split_tokens) {
   Plan p;
-  if (make_plan(B, H, Hkv, D, block_size, max_blocks, max_q_len, dtype, kv_split_tokens, &p) != NSV_OK) return 0;
+  if (make_plan(B, H, Hkv, D, block_size, max_blocks, max_q_len, dtype, kv_split_tokens, device_cus(), &p) != NSV_OK)
+    return 0;
   return workspace_bytes_for(B, Hkv, D, p);
+}
+
+int nsv_verify_attention_plan(int B, int H, int Hkv, int D, int block_size, int max_blocks, int max_q_len, int dtype,
+                              int kv_split_tokens, int cus, int* kernel, int* splits) {
+  Plan p;
+  const int rc = make_plan(B, H, Hkv, D, block_size, max_blocks, max_q_len, dtype, kv_split_tokens,
+                           cus > 0 ? cus : device_cus(), &p);
+  if (rc != NSV_OK) return rc;
+  if (kernel) *kernel = dtype == NSV_F32 ? NSV_ATTN_F32 : (p.ks ? NSV_ATTN_KEY_SPLIT : NSV_ATTN_DSLICED);
+  if (splits) *splits = p.S;
+  return NSV_OK;
 }
 
 int nsv_verify_attention(void* out, const void* q, const void* k_cache, const void* v_cache,
@@ -1531,7 +1542,7 @@ int nsv_verify_attention(void* out, const void* q, const void* k_cache, const vo
                          int max_blocks, int max_q_len, int dtype, int kv_split_tokens, void* workspace,
                          size_t workspace_bytes, void* stream) {
   Plan p;
-  int rc = make_plan(B, H, Hkv, D, block_size, max_blocks, max_q_len, dtype, kv_split_tokens, &p);
+  int rc = make_plan(B, H, Hkv, D, block_size, max_blocks, max_q_len, dtype, kv_split_tokens, device_cus(), &p);
   if (rc != NSV_OK) return rc;
   if (T < 0) return NSV_ERR_ARG;
   if (B == 0 || T == 0) return NSV_OK;

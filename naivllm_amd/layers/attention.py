@@ -47,6 +47,23 @@ def verify_attention_workspace_bytes(batch_size: int, num_heads: int, num_kv_hea
         _lib.dtype_code(dtype), kv_split_tokens))
 
 
+ATTN_KERNELS = {0: "d-sliced", 1: "key-split", 2: "fp32"}
+
+
+def verify_attention_plan(batch_size: int, num_heads: int, num_kv_heads: int, head_dim: int, block_size: int,
+                          max_num_blocks: int, max_q_len: int, dtype: torch.dtype, kv_split_tokens: int = 0,
+                          cus: int = 0) -> tuple[str, int]:
+    """(kernel, key splits per sequence) that paged_attention_verify runs for
+    this shape on a device with ``cus`` compute units (0: the current one)."""
+    import ctypes
+    kind, splits = ctypes.c_int(), ctypes.c_int()
+    rc = _lib.lib().nsv_verify_attention_plan(batch_size, num_heads, num_kv_heads, head_dim, block_size,
+                                             max_num_blocks, max_q_len, _lib.dtype_code(dtype), kv_split_tokens,
+                                             cus, ctypes.addressof(kind), ctypes.addressof(splits))
+    _lib.check(rc, "verify_attention_plan")
+    return ATTN_KERNELS[kind.value], splits.value
+
+
 def paged_attention_verify(
     query: torch.Tensor,
     k_cache: torch.Tensor,

@@ -155,3 +155,20 @@ def config2_ctx_lens(seed: int = 2, batch: int = 8) -> list[int]:
 def config2_batch(seed: int = 2) -> VerifyBatch:
     """BASELINE config 2 attention inputs: b8 bf16, L ~ U[1200,1300], K=8."""
     return verify_batch(seed, config2_ctx_lens(seed), [9] * 8, num_blocks=64, dtype="bf16")
+
+
+def config3_prompts(batch: int, seed: int = 3, prefix: int = 1200, span: int = 40, vocab: int = 151936):
+    """BASELINE config 3 prompts: a 1200-token document made of 40-token
+    spans that recur across it (span i at chapter positions i and 7i mod N,
+    after benchmarks/rag_bench.py:80-105), followed per request by the
+    first tokens of one span as the question, so an answer quoting the
+    document is n-gram draftable."""
+    nspans = 12
+    spans = [[int(x) for x in randint(seed, 90 + i, span, 100, vocab)] for i in range(nspans)]
+    doc = []
+    i = 0
+    while len(doc) < prefix:
+        doc += spans[i % nspans] + spans[(i * 7) % nspans][: span // 4]
+        i += 1
+    doc = doc[:prefix]
+    return [doc + spans[(b * 5 + 1) % nspans][:6] for b in range(batch)]

@@ -55,20 +55,26 @@ def verify_attention(q, k_cache, v_cache, block_tables, context_lens, cu_seqlens
         page = block_tables[b, n // bs].astype(np.int64)
         mapped = page >= 0
         keys = n[mapped]
-        K = np.repeat(k_cache[page[mapped], (n % bs)[mapped]].astype(np.float64), G, axis=1)  # [Lk, H, D]
-        V = np.repeat(v_cache[page[mapped], (n % bs)[mapped]].astype(np.float64), G, axis=1)
-        for r in range(r0, r1):
-            pos = int(positions[r])
-            if pos < 0:
-                continue
-            sel = keys <= pos
-            if not sel.any():
-                continue
-            s = np.einsum("hd,khd->hk", q[r], K[sel]) * scale
-            s -= s.max(axis=1, keepdims=True)
-            p = np.exp(s)
-            p /= p.sum(axis=1, keepdims=True)
-            out[r] = np.einsum("hk,khd->hd", p, V[sel])
+        rows = [r for r in range(r0, r1) if int(positions[r]) >= 0]
+        if not rows or keys.size == 0:
+            continue
+        pos = np.array([int(positions[r]) for r in rows])
+        visible = keys[None, :] <= pos[:, None]  # [rows, Lk]
+        for hk in range(hkv):  # kv head hk serves query heads hk*G .. hk*G+G-1
+            K = k_cache[page[mapped], (n % bs)[mapped], hk].astype(np.float64)  # [Lk, D]
+            V = v_cache[page[mapped], (n % bs)[mapped], hk].astype(np.float64)
+            for g in range(G):
+                h = hk * G + g
+                s = (q[rows, h] @ K.T) * scale  # [rows, Lk]
+                s = np.where(visible, s, -np.inf)
+                m = s.max(axis=1, keepdims=True)
+                ok = np.isfinite(m[:, 0])  # a row with no visible key keeps zeros
+                p = np.exp(s - np.where(np.isfinite(m), m, 0.0))
+                p /= np.maximum(p.sum(axis=1, keepdims=True), 1e-300)
+                o = p @ V
+                for i, r in enumerate(rows):
+                    if ok[i]:
+                        out[r, h] = o[i]
     return out
 
 

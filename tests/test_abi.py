@@ -151,3 +151,49 @@ def test_linear_rejects_bad_arguments_before_launch():
     assert n >= 64 * 4 * 80 * 16 * 4
     assert h.nsv_linear(1, None, None, 0, 1e-6, 1, 1, None, None, 72, 1024, 2048, 0, None, 0, None) == -3
     assert h.nsv_linear_workspace_size(72, 4096, 1024) == 0  # 256 tiles cover the chip without a split
+
+
+def linear_plan(M, N, K, norm, epi, cus):
+    import ctypes
+    cols, ks, half = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    rc = _lib.lib().nsv_linear_plan(M, N, K, int(norm), epi, cus, ctypes.addressof(cols), ctypes.addressof(ks),
+                                    ctypes.addressof(half))
+    assert rc == 0
+    return cols.value, ks.value, half.value
+
+
+def test_linear_split_only_with_16_column_tiles():
+    """A split reduction (ks > 1) is merged only by the 16-column kernel: the
+    8- and 32-column kernels deal the reduction to one workgroup.  Sweep the
+    dispatch over shapes and CU counts, including partitions with fewer than
+    128 CUs, where wide SwiGLU grids and split reductions could both apply."""
+    h = _lib.lib()
+    seen = set()
+    for cus in (20, 38, 64, 80, 100, 127, 128, 200, 256, 304):
+        for M in (1, 9, 16, 17, 31, 32, 33, 48, 72, 80, 81, 160):
+            for N in (256, 1024, 1536, 2048, 3072, 4096, 6144, 12288, 24576):
+                for K in (256, 1024, 2048, 4096):
+                    for norm in (False, True):
+                        for epi in (0, 1, 2):
+                            cols, ks, half = linear_plan(M, N, K, norm, epi, cus)
+                            seen.add((cols, ks > 1))
+                            assert cols in (8, 16, 32)
+                            if cols != 16:
+                                assert ks == 1, (cus, M, N, K, norm, epi, cols, ks)
+                            if cols == 32:
+                                assert epi == 1 and N // 16 >= 128
+                            if cols == 8:
+                                assert not norm and epi != 1 and M <= 31
+                            ws = h.nsv_linear_workspace_size(M, N, K)
+                            assert (ws > 0) == (ks > 1), (cus, M, N, K, ks, ws)
+    assert {(8, False), (16, False), (16, True), (32, False)} <= seen
+
+
+def test_linear_plan_rejects_bad_shapes():
+    import ctypes
+    x = ctypes.c_int()
+    h = _lib.lib()
+    p = ctypes.addressof(x)
+    assert h.nsv_linear_plan(9, 100, 1024, 0, 0, 256, p, p, p) == -1  # N not a multiple of 16
+    assert h.nsv_linear_plan(9, 1024, 1020, 0, 0, 256, p, p, p) == -1  # K not a multiple of 8
+    assert h.nsv_linear_plan(9, 1024, 1024, 0, 3, 256, p, p, p) == -1  # no epilogue 3

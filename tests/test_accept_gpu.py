@@ -9,7 +9,7 @@ from naivllm_amd.spec_engine import RejectionSampler
 from naivllm_amd.spec_engine.rejection_sampler import accept_greedy, accept_stochastic, draw_randomness, sample
 from naivllm_amd.utils import synth
 from oracle import accept as oa
-from tests.test_oracle_accept import reference_torch
+from oracle.torch_cpu import verify_stochastic as reference_torch
 
 pytestmark = pytest.mark.gpu
 

@@ -81,8 +81,9 @@ def test_linear_plain(M, N, K, norm):
 
 
 # I >= 2080 puts more than 256 16-column tiles on the grid, which takes the
-# 32-column tiles (16 gate + 16 up rows) on up to 256 of them, or beyond 16
-# rows; (9, 12288, 4096) keeps the 16-column tiles; 90 rows take two row blocks
+# 32-column tiles (16 gate + 16 up rows); (9, 12288, 4096) and (20, 12288,
+# 4096) run them with half chunks (two workgroups per CU at 9 rows, one at
+# 20); 90 rows take two row blocks
 @pytest.mark.parametrize("M,I,K,norm", [(9, 3072, 1024, True), (72, 3072, 1024, True), (5, 128, 256, True),
                                         (90, 256, 512, True), (40, 256, 1024, True), (18, 3072, 1024, True),
                                         (36, 3072, 1024, False), (50, 3072, 1024, True), (90, 3072, 1024, True),

@@ -7,42 +7,10 @@ import pytest
 import torch
 
 from oracle import accept as oa
+from oracle.torch_cpu import sample as sampler_torch
+from oracle.torch_cpu import verify_stochastic as reference_torch
 
 TDT = {"bf16": torch.bfloat16, "f32": torch.float32}
-
-
-def reference_torch(draft_tokens, target_rows, draft_rows, temperature, g):
-    """The reference's sequence of torch calls (rejection_sampler.py:38-85),
-    executed by torch on the device of its inputs with generator g — an
-    independent computation path (torch's softmax, multinomial and dtype
-    promotion)."""
-    p_target = torch.softmax(target_rows / temperature, dim=-1)
-    K = len(draft_tokens)
-    acc = []
-    if draft_rows is not None:
-        p_draft = torch.softmax(draft_rows / temperature, dim=-1)
-        ids = torch.tensor(draft_tokens, device=target_rows.device, dtype=torch.long)
-        pd = p_draft.gather(1, ids[:, None]).squeeze(1)
-        pt = p_target[:-1].gather(1, ids[:, None]).squeeze(1)
-        ratio = (pt / pd.clamp_min(1e-20)).clamp(max=1.0)
-        u = torch.rand(K, device=target_rows.device, generator=g)
-        for i in range(K):
-            if u[i] < ratio[i]:
-                acc.append(draft_tokens[i])
-                continue
-            r = (p_target[i] - p_draft[i]).clamp_min(0)
-            if r.sum() <= 0:
-                r = p_target[i]
-            acc.append(int(torch.multinomial(r / r.sum(), 1, generator=g).item()))
-            return acc
-        acc.append(int(torch.multinomial(p_target[K], 1, generator=g).item()))
-        return acc
-    s = torch.multinomial(p_target, 1, generator=g).squeeze(1).tolist()
-    for i in range(K):
-        if s[i] != draft_tokens[i]:
-            return acc + [s[i]]
-        acc.append(draft_tokens[i])
-    return acc + [s[K]]
 
 
 def draw_noise(K, V, dtype, g, with_draft_rows):
@@ -169,17 +137,6 @@ def test_stochastic_closed_forms():
     assert len(out) == 1 and out[0] != 7
     # temperature <= 1e-6 dispatches to greedy (rejection_sampler.py:95)
     assert oa.verify([int(np.argmax(x[0])), 0], x[:3], temperature=0.0)[0] == int(np.argmax(x[0]))
-
-
-def sampler_torch(logits, temperature, noise):
-    """layers/sampler.py:14-24's torch calls, executed by torch (an
-    independent path: torch's fp32 softmax and promotion rules)."""
-    greedy = temperature <= 1e-6
-    safe_temperature = torch.where(greedy, torch.ones_like(temperature), temperature)
-    argmax_tokens = logits.argmax(dim=-1)
-    probs = torch.softmax(logits / safe_temperature.unsqueeze(-1), dim=-1)
-    sample_tokens = (probs / noise).argmax(dim=-1)
-    return torch.where(greedy, argmax_tokens, sample_tokens)
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
