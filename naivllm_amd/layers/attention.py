@@ -115,9 +115,9 @@ def paged_attention_verify(
     batch_size, max_num_blocks = block_tables.shape
     qlen_bound = int(max_q_len if max_q_len is not None else block_m)
     code = _lib.dtype_code(query.dtype)
+    h = _lib.lib()
     if out is None:
         out = torch.empty_like(query)
-    h = _lib.lib()
     ws_bytes = int(h.nsv_verify_attention_workspace_size(
         batch_size, num_heads, num_kv_heads, head_dim, block_size, max_num_blocks, qlen_bound, code,
         kv_split_tokens))
@@ -165,10 +165,17 @@ def store_kvcache(
 
 
 class Attention(nn.Module):
-    """Verify-mode attention layer (layers/attention.py:674-731): writes this
-    step's K/V into the paged cache, then runs verify attention for the rows
-    described by the global Context.  Only the verify / decode (q_len 1)
-    modes of the round are served here."""
+    """Attention layer of the reference (layers/attention.py:670-767):
+    writes this step's K/V into the paged cache at context.slot_mapping,
+    then attends from the query rows the global Context describes:
+      * verify (context.is_verify): a chunk of drafted tokens per sequence
+        with a causal mask from absolute positions (:704-731);
+      * decode (neither flag): one query row per sequence attending its
+        whole context (:759-767), served by the same verify kernel with
+        each row at position context_lens - 1.
+    Prefill (context.is_prefill) is not a mode of this class: the verify
+    forward (naivllm_amd.layers.qwen3) prefills prompts through its own
+    chunked path."""
 
     def __init__(self, num_heads: int, head_dim: int, scale: float = 1.0, num_kv_heads: int | None = None,
                  block_size: int = 16):
@@ -187,14 +194,21 @@ class Attention(nn.Module):
             store_kvcache(k.reshape(-1, self.num_kv_heads, self.head_dim),
                           v.reshape(-1, self.num_kv_heads, self.head_dim),
                           k_cache, v_cache, context.slot_mapping, self.block_size)
-        if not context.is_verify:
-            raise ValueError("naivllm_amd.Attention serves the verify round only (context.is_verify)")
+        if context.is_prefill and not context.is_verify:
+            raise ValueError("naivllm_amd.Attention serves verify and decode steps; prefill runs through the "
+                             "verify forward's chunked path")
         scale = self.scale / (self.head_dim ** 0.5)
-        max_q_len = max(context.seqlens_q)
-        block_m = max(16, 1 << (max_q_len - 1).bit_length())
         q = q.reshape(-1, self.num_heads, self.head_dim)
+        if context.is_verify:
+            max_q_len = max(context.seqlens_q)
+            cu, positions = context.cu_seqlens_q, context.positions
+        else:
+            # decode: row b is the newest token of sequence b
+            max_q_len = 1
+            cu = torch.arange(0, q.shape[0] + 1, dtype=torch.int32, device=q.device)
+            positions = context.context_lens.to(torch.int64) - 1
+        block_m = max(16, 1 << (max_q_len - 1).bit_length())
         o = paged_attention_verify(
-            q, k_cache, v_cache, context.block_tables, context.context_lens, context.cu_seqlens_q,
-            context.positions, scale, self.num_heads, self.num_kv_heads, self.head_dim, self.block_size,
-            block_m, max_q_len=max_q_len)
+            q, k_cache, v_cache, context.block_tables, context.context_lens, cu, positions, scale,
+            self.num_heads, self.num_kv_heads, self.head_dim, self.block_size, block_m, max_q_len=max_q_len)
         return o.reshape(o.shape[0], self.num_heads * self.head_dim)
