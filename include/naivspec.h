@@ -35,6 +35,8 @@ extern "C" {
 #define NSV_ERR_ARG (-1)         /* null pointer, negative size, bad dtype  */
 #define NSV_ERR_UNSUPPORTED (-2) /* shape outside what the kernels handle   */
 #define NSV_ERR_WORKSPACE (-3)   /* workspace pointer null or too small     */
+#define NSV_ERR_SCRATCH (-4)     /* shape beyond the allocation-free entry  */
+                                 /* point's fixed scratch                    */
 
 /* Library version (major*10000 + minor*100 + patch). */
 int nsv_version(void);
@@ -81,6 +83,32 @@ int nsv_verify_attention(void* out, const void* q, const void* k_cache,
                          int block_size, int max_blocks, int max_q_len,
                          int dtype, int kv_split_tokens, void* workspace,
                          size_t workspace_bytes, void* stream);
+
+/*
+ * Allocation-free variant of nsv_verify_attention: same arguments and
+ * results, minus the workspace.  No reference counterpart: it is for callers
+ * that cannot allocate device memory (code under hipGraph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  Its scratch is a fixed
+ * device array of nsv_verify_attention_noalloc_max_scratch() bytes (16 MiB)
+ * inside the library, one per device, held until the process ends; a shape
+ * whose nsv_verify_attention_workspace_size() exceeds it is rejected with
+ * NSV_ERR_SCRATCH before anything is launched.  Never calls hipMalloc,
+ * hipFree or an allocating library routine; the first call on a device
+ * looks the array up and enqueues a clear of its counter area on `stream`.
+ * Every call on a device shares that device's array: calls that overlap on
+ * one GPU (concurrent streams, or host threads) race and must be ordered by
+ * the caller, as calls sharing a workspace must be.
+ */
+size_t nsv_verify_attention_noalloc_max_scratch(void);
+int nsv_verify_attention_noalloc(void* out, const void* q, const void* k_cache,
+                                 const void* v_cache,
+                                 const int32_t* block_tables,
+                                 const int64_t* context_lens,
+                                 const int32_t* cu_seqlens_q,
+                                 const int64_t* positions, float scale, int B,
+                                 int T, int H, int Hkv, int D, int block_size,
+                                 int max_blocks, int max_q_len, int dtype,
+                                 int kv_split_tokens, void* stream);
 
 /* The kernel nsv_verify_attention runs for these arguments on a device
  * with `cus` compute units (cus <= 0: the current device) and the key

@@ -33,6 +33,10 @@ SIGNATURES: dict[str, tuple] = {
     "nsv_verify_attention": (
         _c_int,
         [_c_vp] * 8 + [_c_f32] + [_c_int] * 10 + [_c_vp, _c_size, _c_vp]),
+    "nsv_verify_attention_noalloc_max_scratch": (_c_size, []),
+    "nsv_verify_attention_noalloc": (
+        _c_int,
+        [_c_vp] * 8 + [_c_f32] + [_c_int] * 10 + [_c_vp]),
     "nsv_store_kv": (_c_int, [_c_vp] * 5 + [_c_int] * 5 + [_c_vp]),
     "nsv_accept_workspace_size": (_c_size, [_c_int] * 5),
     "nsv_accept_greedy": (

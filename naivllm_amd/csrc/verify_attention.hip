@@ -28,6 +28,8 @@
 
 #include "common.h"
 
+#include <mutex>
+
 namespace {
 
 constexpr int kTile = 32;   // keys per wave iteration
@@ -1501,6 +1503,51 @@ void launch_f32(const VerifyArgs& a, int D, dim3 grid, hipStream_t s) {
     hipLaunchKernelGGL((verify_attn_f32_kernel<MT, 64>), grid, dim3(64), 0, s, a);
 }
 
+// ---------------------------------------------------------------------------
+// Scratch of the allocation-free entry point (nsv_verify_attention_noalloc).
+// ---------------------------------------------------------------------------
+// A fixed device array holds what the caller's workspace holds otherwise:
+// the arrival-counter area, then the split partials.  Every device the
+// library runs on gets its own copy, at its own address, for the life of
+// the process.  Device globals start zeroed and every call leaves the
+// counters zero, the invariant the workspace contract already relies on.
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+static __device__ __attribute__((aligned(256))) unsigned char scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+__global__ void clear_counters_kernel(unsigned* counters, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) counters[i] = 0u;
+}
+
+// The current device's copy of `scratch`, looked up once per device with
+// that device current (the array's name in host code is a host-side handle,
+// not a device address).  The first lookup on a device also enqueues a
+// clear of the counter area on `stream` (a kernel, so that a caller
+// capturing the stream records no memset node).  Returns a hipError_t.
+int scratch_for_current_device(hipStream_t stream, void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxScratchDevices) return NSV_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr) return e != hipSuccess ? (int)e : (int)hipErrorInvalidSymbol;
+    hipLaunchKernelGGL(clear_counters_kernel, dim3((kMaxCounterPairs + 255) / 256), dim3(256), 0, stream,
+                       (unsigned*)ptr, kMaxCounterPairs);
+    const int rc = nsv_launch_status();
+    if (rc != NSV_OK) return rc;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return NSV_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1513,6 +1560,7 @@ const char* nsv_error_string(int code) {
     case NSV_ERR_ARG: return "invalid argument";
     case NSV_ERR_UNSUPPORTED: return "unsupported shape";
     case NSV_ERR_WORKSPACE: return "workspace missing or too small";
+    case NSV_ERR_SCRATCH: return "shape needs more scratch than the allocation-free entry point holds";
     default: return code > 0 ? hipGetErrorString((hipError_t)code) : "unknown error";
   }
 }
@@ -1615,6 +1663,25 @@ int nsv_verify_attention(void* out, const void* q, const void* k_cache, const vo
     else hipLaunchKernelGGL((verify_merge_kernel<float, 1>), mgrid, dim3(256), 0, s, a);
   }
   return nsv_launch_status();
+}
+
+size_t nsv_verify_attention_noalloc_max_scratch(void) { return kNoAllocScratchBytes; }
+
+int nsv_verify_attention_noalloc(void* out, const void* q, const void* k_cache, const void* v_cache,
+                                 const int32_t* block_tables, const int64_t* context_lens,
+                                 const int32_t* cu_seqlens_q, const int64_t* positions, float scale, int B, int T,
+                                 int H, int Hkv, int D, int block_size, int max_blocks, int max_q_len, int dtype,
+                                 int kv_split_tokens, void* stream) {
+  Plan p;
+  int rc = make_plan(B, H, Hkv, D, block_size, max_blocks, max_q_len, dtype, kv_split_tokens, device_cus(), &p);
+  if (rc != NSV_OK) return rc;
+  if (workspace_bytes_for(B, Hkv, D, p) > kNoAllocScratchBytes) return NSV_ERR_SCRATCH;
+  void* ws = nullptr;
+  rc = scratch_for_current_device((hipStream_t)stream, &ws);
+  if (rc != NSV_OK) return rc;
+  return nsv_verify_attention(out, q, k_cache, v_cache, block_tables, context_lens, cu_seqlens_q, positions, scale,
+                              B, T, H, Hkv, D, block_size, max_blocks, max_q_len, dtype, kv_split_tokens, ws,
+                              kNoAllocScratchBytes, stream);
 }
 
 int nsv_store_kv(const void* key, const void* value, void* k_cache, void* v_cache, const int64_t* slot_mapping,

@@ -82,6 +82,7 @@ def paged_attention_verify(
     max_q_len: int | None = None,
     kv_split_tokens: int = 0,
     out: torch.Tensor | None = None,
+    allocation_free: bool = False,
 ) -> torch.Tensor:
     """Verify a chunk of drafted tokens against the paged KV cache.
 
@@ -92,9 +93,13 @@ def paged_attention_verify(
       block_m >= every per-sequence query length.
     Returns (T, H, D) in query's dtype.  Keyword-only extras: ``max_q_len``
     (a tighter bound than block_m: fewer padded MFMA rows and partials),
-    ``kv_split_tokens`` (keys per workgroup split, 0 = automatic) and ``out``
-    (a preallocated result).  Rows at position -1 come back as zeros (the
-    reference leaves them meaningless; nothing reads them).
+    ``kv_split_tokens`` (keys per workgroup split, 0 = automatic), ``out``
+    (a preallocated result) and ``allocation_free`` (run through
+    nsv_verify_attention_noalloc: the library's fixed per-device scratch
+    instead of a workspace, ``out`` required, index tensors already int32 /
+    int64 and contiguous, so the call allocates nothing).  Rows at position
+    -1 come back as zeros (the reference leaves them meaningless; nothing
+    reads them).
     """
     if query.dim() != 3 or query.shape[1] != num_heads or query.shape[2] != head_dim:
         raise ValueError(f"query must be (T, {num_heads}, {head_dim}), got {tuple(query.shape)}")
@@ -116,6 +121,16 @@ def paged_attention_verify(
     qlen_bound = int(max_q_len if max_q_len is not None else block_m)
     code = _lib.dtype_code(query.dtype)
     h = _lib.lib()
+    if allocation_free:
+        if out is None:
+            raise ValueError("allocation_free=True needs a preallocated out")
+        rc = h.nsv_verify_attention_noalloc(
+            out.data_ptr(), query.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), block_tables.data_ptr(),
+            context_lens.data_ptr(), cu_seqlens_q.data_ptr(), positions.data_ptr(), float(scale), batch_size,
+            query.shape[0], num_heads, num_kv_heads, head_dim, block_size, max_num_blocks, qlen_bound, code,
+            kv_split_tokens, _lib.stream_ptr(query.device))
+        _lib.check(rc, "paged_attention_verify (allocation-free)")
+        return out
     if out is None:
         out = torch.empty_like(query)
     ws_bytes = int(h.nsv_verify_attention_workspace_size(

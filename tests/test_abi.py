@@ -197,3 +197,18 @@ def test_linear_plan_rejects_bad_shapes():
     assert h.nsv_linear_plan(9, 100, 1024, 0, 0, 256, p, p, p) == -1  # N not a multiple of 16
     assert h.nsv_linear_plan(9, 1024, 1020, 0, 0, 256, p, p, p) == -1  # K not a multiple of 8
     assert h.nsv_linear_plan(9, 1024, 1024, 0, 3, 256, p, p, p) == -1  # no epilogue 3
+
+
+def test_no_alloc_entry_rejects_shapes_beyond_its_scratch():
+    # a 64-sequence fp32 batch over 128-page tables needs ~19 MB of split
+    # partials, beyond the allocation-free entry point's 16 MiB: rejected
+    # before anything is launched (no device pointer is touched)
+    h = _lib.lib()
+    assert h.nsv_verify_attention_noalloc_max_scratch() == 16 << 20
+    need = h.nsv_verify_attention_workspace_size(64, 16, 8, 128, 256, 128, 9, 0, 0)
+    assert need > 16 << 20
+    rc = h.nsv_verify_attention_noalloc(1, 1, 1, 1, 1, 1, 1, 1, 0.1, 64, 576, 16, 8, 128, 256, 128, 9, 0, 0, None)
+    assert rc == -4
+    assert h.nsv_error_string(-4) == b"shape needs more scratch than the allocation-free entry point holds"
+    # shapes the plan refuses keep their own codes
+    assert h.nsv_verify_attention_noalloc(1, 1, 1, 1, 1, 1, 1, 1, 0.1, 8, 72, 16, 8, 96, 256, 6, 9, 1, 0, None) == -2
