@@ -701,8 +701,10 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
   constexpr int RSTR = DH + 4;    // merge-region row stride (floats)
   constexpr int KSTAGE = WROW ? NW * TK * DH * 2 : 0;  // whole-row K tiles
   constexpr int STAGE = NW * TK * VSTR * 2 + KSTAGE;
-  constexpr int MTILE_BYTES = NW * 16 * RSTR * 4;
-  constexpr int SMEM = STAGE > MTILE_BYTES ? STAGE : MTILE_BYTES;
+  constexpr int MROWS = MP < 32 ? MP : 32;  // query rows one merge pass covers
+  constexpr int MPASS = (MP + MROWS - 1) / MROWS;
+  constexpr int MERGE_BYTES = NW * MROWS * RSTR * 4;  // every wave's O for MROWS rows
+  constexpr int SMEM = STAGE > MERGE_BYTES ? STAGE : MERGE_BYTES;
 
   __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM];
   __shared__ int pages[kMaxSplitPages];
@@ -951,22 +953,55 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
     __builtin_amdgcn_wave_barrier();
   };
 
-  // ---- NS-stage pipeline over this wave's tiles
-  Tile T[NS];
+  // ---- pipeline over this wave's tiles
   load_q();
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int s = 0; s < NS; ++s) issue(T[s], s);
-  __builtin_amdgcn_sched_barrier(0);
-  finish_positions();
-  store_q();
-  lds_barrier();  // query rows visible; the tile loads stay in flight
-  for (int it = 0; it < niter; it += NS) {
-#pragma unroll
-    for (int s = 0; s < NS; ++s) {
+  if constexpr (NS == 1) {
+    // Short splits (a few tiles per wave): at most one tile in flight per
+    // wave, and the next tile is issued as soon as the current one has
+    // landed, before it is computed, so the arithmetic hides under the next
+    // tile's flight.  (More tiles in flight only queue more requests at the
+    // same bandwidth: on MI355X at config 2 the loads alone take 9.2 us
+    // with one tile per wave in flight, 9.6 with two, 10.3 with four.)
+    Tile T0, T1;
+    __builtin_amdgcn_sched_barrier(0);
+    issue(T0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    finish_positions();
+    store_q();
+    lds_barrier();  // query rows visible; the first tile stays in flight
+    for (int it = 0; it < niter; it += 2) {
+      __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): tile it landed
       __builtin_amdgcn_sched_barrier(0);
-      compute(T[s]);
-      issue(T[s], it + s + NS);
+      if (it + 1 < niter) issue(T1, it + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(T0);
+      if (it + 1 >= niter) break;
+      __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): tile it + 1 landed
+      __builtin_amdgcn_sched_barrier(0);
+      if (it + 2 < niter) issue(T0, it + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(T1);
+    }
+  } else {
+    // Long splits: an NS-stage register pipeline (the next NS tiles in
+    // flight while one computes).  Every issue is unconditional (tiles past
+    // the split read a mapped row), which keeps the compiler's wait counts
+    // exact across iterations.
+    Tile T[NS];
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < NS; ++s) issue(T[s], s);
+    __builtin_amdgcn_sched_barrier(0);
+    finish_positions();
+    store_q();
+    lds_barrier();  // query rows visible; the tile loads stay in flight
+    for (int it = 0; it < niter; it += NS) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        __builtin_amdgcn_sched_barrier(0);
+        compute(T[s]);
+        issue(T[s], it + s + NS);
+      }
     }
   }
 
@@ -978,56 +1013,83 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
       red_l[w][mt * 16 + c] = l_run[mt];
     }
   }
-  __syncthreads();  // also: every wave is done with its V staging rows
-  if (tid < MP) {
-    float M = kNegInf;
-#pragma unroll
-    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, red_m[ww][tid]);
-    const float ref = (M == kNegInf) ? 0.f : M;
-    float L = 0.f;
-#pragma unroll
-    for (int ww = 0; ww < NW; ++ww) L += red_l[ww][tid] * __builtin_amdgcn_exp2f((red_m[ww][tid] - ref) * sc);
-    row_ms[tid] = M == kNegInf ? kNegInf : M * sc;  // partials carry the log2-domain max
-    row_l[tid] = L;
-  }
+  __syncthreads();  // also: every wave is done with its staging rows
+  // every lane: the split's max over the waves for its rows, and its own
+  // waves' rescale factor; wave 0 keeps the split's (max, sum) per row
   float fac[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int m = mt * 16 + c;
+    float rm[NW];
     float M = kNegInf;
 #pragma unroll
-    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, red_m[ww][m]);
-    fac[mt] = __builtin_amdgcn_exp2f((m_run[mt] - ((M == kNegInf) ? 0.f : M)) * sc);
+    for (int ww = 0; ww < NW; ++ww) {
+      rm[ww] = red_m[ww][m];
+      M = fmaxf(M, rm[ww]);
+    }
+    const float ref = (M == kNegInf) ? 0.f : M;
+    fac[mt] = __builtin_amdgcn_exp2f((m_run[mt] - ref) * sc);
+    if (w == 0 && g4 == 0) {
+      float L = 0.f;
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww) L = fmaf(red_l[ww][m], __builtin_amdgcn_exp2f((rm[ww] - ref) * sc), L);
+      const float ms = M == kNegInf ? kNegInf : M * sc;  // partials carry the log2-domain max
+      row_ms[m] = ms;
+      row_l[m] = L;
+      if (nsplit > 1 && m < a.Mv) {
+        const bool real = row_pos[m] >= 0;
+        store_agent(reinterpret_cast<uint64_t*>(&a.part_ml[(((int64_t)pair * a.S + split) * a.Mv + m) * 2]),
+                    real ? ms : kNegInf, real ? L : 0.f);
+      }
+    }
   }
-  float* region = reinterpret_cast<float*>(smem);  // [NW][16][RSTR], one m-tile per pass
+  // Every wave's scaled O rows (real rows only: rows >= Mv are padding) go
+  // to LDS, MROWS rows per pass (one pass up to 32 rows); then thread tid
+  // sums the waves for items (row, 4 dims) tid, tid + NT, ... of the pass.
+  // The items a thread sums (ITEMS per pass) are the ones it merges across
+  // splits below, so its own split's sums stay in registers.
+  float* region = reinterpret_cast<float*>(smem);  // [NW][MROWS][RSTR]
   constexpr int C4 = DH / 4;
+  constexpr int ITEMS = (MROWS * C4 + NT - 1) / NT;
+  f32x4 own[MPASS][ITEMS];
   const int64_t pbase = ((int64_t)pair * a.S + split) * a.Mv;
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    __syncthreads();  // staging rows / the previous pass fully read
-    // lane (g4, c) element i of tile (dt, mt) is O[16 mt + c][16 dt + 4 g4 + i]
+  for (int ps = 0; ps < MPASS; ++ps) {
+    if (ps > 0) __syncthreads();  // the previous pass fully read
 #pragma unroll
-    for (int dt = 0; dt < DT; ++dt)
-      *reinterpret_cast<f32x4*>(&region[(w * 16 + c) * RSTR + dt * 16 + g4 * 4]) = acc[dt][mt] * fac[mt];
+    for (int mt = ps * (MROWS / 16); mt < MT && mt < (ps + 1) * (MROWS / 16); ++mt) {
+      const int m = mt * 16 + c;
+      if (m < a.Mv) {
+        // lane (g4, c) element i of tile (dt, mt) is O[16 mt + c][16 dt + 4 g4 + i]
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+          *reinterpret_cast<f32x4*>(&region[(w * MROWS + (m - ps * MROWS)) * RSTR + dt * 16 + g4 * 4]) =
+              acc[dt][mt] * fac[mt];
+      }
+    }
     __syncthreads();
-    for (int qd = tid; qd < 16 * C4; qd += NT) {
-      const int r = qd / C4, c4 = qd - r * C4;
-      const int m = mt * 16 + r;
-      if (m >= a.Mv) continue;
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+      const int qd = tid + j * NT;
+      const int r = qd / C4, c4 = qd % C4;
+      const int m = ps * MROWS + r;
+      own[ps][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (r >= MROWS || m >= a.Mv) continue;
       f32x4 o = *reinterpret_cast<const f32x4*>(&region[r * RSTR + c4 * 4]);
 #pragma unroll
-      for (int ww = 1; ww < NW; ++ww) o += *reinterpret_cast<const f32x4*>(&region[(ww * 16 + r) * RSTR + c4 * 4]);
+      for (int ww = 1; ww < NW; ++ww) o += *reinterpret_cast<const f32x4*>(&region[(ww * MROWS + r) * RSTR + c4 * 4]);
+      if (row_pos[m] < 0) o = f32x4{0.f, 0.f, 0.f, 0.f};
+      own[ps][j] = o;
       if (nsplit == 1) {
         const int g = m / a.QL, t = m - g * a.QL;
         if (t >= qlen) continue;
         const float L = row_l[m];
-        const float inv = (L > 0.f && row_pos[m] >= 0) ? 1.f / L : 0.f;
+        const float inv = L > 0.f ? 1.f / L : 0.f;
         bf16_t* dst = (bf16_t*)a.out + ((int64_t)(q0 + t) * a.H + hk * a.G + g) * DH + c4 * 4;
         const uint32_t lo = (uint32_t)f32_to_bf16_bits(o[0] * inv) | ((uint32_t)f32_to_bf16_bits(o[1] * inv) << 16);
         const uint32_t hi = (uint32_t)f32_to_bf16_bits(o[2] * inv) | ((uint32_t)f32_to_bf16_bits(o[3] * inv) << 16);
         *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
       } else {
-        if (row_pos[m] < 0) o = f32x4{0.f, 0.f, 0.f, 0.f};
         uint64_t* dst = reinterpret_cast<uint64_t*>(&a.part_o[(pbase + m) * DH + c4 * 4]);
         store_agent(dst, o[0], o[1]);
         store_agent(dst + 1, o[2], o[3]);
@@ -1042,10 +1104,6 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
   // them are acknowledged the split counts itself in; the split that counts
   // last reads every partial back with agent-scope loads, so no cache
   // write-back or invalidation of a whole L2 is needed.
-  if (tid < a.Mv) {
-    uint64_t* dst = reinterpret_cast<uint64_t*>(&a.part_ml[(pbase + tid) * 2]);
-    store_agent(dst, row_pos[tid] >= 0 ? row_ms[tid] : kNegInf, row_pos[tid] >= 0 ? row_l[tid] : 0.f);
-  }
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   __shared__ int is_last;
@@ -1055,52 +1113,115 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
   __syncthreads();
   if (!is_last) return;
   if (tid == 0) __hip_atomic_store(&a.counters[pair], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  constexpr int C2 = DH / 2;
-  constexpr int CH = 8;  // splits per round trip
+  // The other splits' partials and (max, sum) pairs for this thread's items,
+  // loaded CH splits per round trip (all loads of a round trip issued before
+  // any is used); this split's own sums are still in registers.
   const int64_t base0 = (int64_t)pair * a.S * a.Mv;  // row 0 of split 0
-  for (int qd = tid; qd < a.Mv * C2; qd += NT) {
-    const int m = qd / C2, c2 = qd - m * C2;
+  constexpr int CH = 4;
+  // Up to CH splits: every value this thread merges, for all its items,
+  // is loaded in one round trip (all loads issued before any is used).
+  // Splits fold in a fixed order (0, 1, ...), whichever split merges, so
+  // the result does not depend on which split finished last.
+  auto fold = [&](float& M, float& den, f32x4& num, float ms, float ls, f32x4 os) {
+    const float Mn = fmaxf(M, ms);
+    if (Mn == kNegInf) return;  // no key of this row so far
+    const float a0 = exp2f(M - Mn), a1 = exp2f(ms - Mn);  // -inf: 0
+    den = den * a0 + ls * a1;
+    num = num * a0 + os * a1;
+    M = Mn;
+  };
+  auto write_out = [&](int m, int c4, float den, f32x4 num) {
     const int g = m / a.QL, t = m - g * a.QL;
-    if (t >= qlen) continue;
-    float M = kNegInf, den = 0.f, n0 = 0.f, n1 = 0.f;
-    for (int s0 = 0; s0 < nsplit; s0 += CH) {
-      float ms[CH], ls[CH], o0[CH], o1[CH];
-#pragma unroll
-      for (int j = 0; j < CH; ++j) {
-        const int sp = s0 + j < nsplit ? s0 + j : s0;
-        const int64_t r = base0 + (int64_t)sp * a.Mv + m;
-        const float2 ml = load_agent(reinterpret_cast<const uint64_t*>(&a.part_ml[r * 2]));
-        const float2 ov = load_agent(reinterpret_cast<const uint64_t*>(&a.part_o[r * DH + c2 * 2]));
-        ms[j] = s0 + j < nsplit ? ml.x : kNegInf;
-        ls[j] = ml.y;
-        o0[j] = ov.x;
-        o1[j] = ov.y;
-      }
-      float Mn = M;
-#pragma unroll
-      for (int j = 0; j < CH; ++j) Mn = fmaxf(Mn, ms[j]);
-      if (Mn == kNegInf) continue;  // no key of this row so far
-      const float rs = exp2f(M - Mn);  // M = -inf: 0 (nothing accumulated yet)
-      den *= rs;
-      n0 *= rs;
-      n1 *= rs;
-#pragma unroll
-      for (int j = 0; j < CH; ++j) {
-        const float wgt = exp2f(ms[j] - Mn);  // -inf (absent split, row without keys): 0
-        den = fmaf(wgt, ls[j], den);
-        n0 = fmaf(wgt, o0[j], n0);
-        n1 = fmaf(wgt, o1[j], n1);
-      }
-      M = Mn;
-    }
     const float inv = den > 0.f ? 1.f / den : 0.f;
-    bf16_t* dst = (bf16_t*)a.out + ((int64_t)(q0 + t) * a.H + hk * a.G + g) * DH + c2 * 2;
-    *reinterpret_cast<uint32_t*>(dst) =
-        (uint32_t)f32_to_bf16_bits(n0 * inv) | ((uint32_t)f32_to_bf16_bits(n1 * inv) << 16);
+    bf16_t* dst = (bf16_t*)a.out + ((int64_t)(q0 + t) * a.H + hk * a.G + g) * DH + c4 * 4;
+    const uint32_t lo = (uint32_t)f32_to_bf16_bits(num[0] * inv) | ((uint32_t)f32_to_bf16_bits(num[1] * inv) << 16);
+    const uint32_t hi = (uint32_t)f32_to_bf16_bits(num[2] * inv) | ((uint32_t)f32_to_bf16_bits(num[3] * inv) << 16);
+    *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+  };
+  auto item_ok = [&](int ps, int j, int& m, int& c4) {
+    const int qd = tid + j * NT;
+    const int r = qd / C4;
+    c4 = qd % C4;
+    m = ps * MROWS + r;
+    if (r >= MROWS || m >= a.Mv) return false;
+    return m - (m / a.QL) * a.QL < qlen;
+  };
+  if (nsplit <= CH) {
+    float2 ml[MPASS][ITEMS][CH], o01[MPASS][ITEMS][CH], o23[MPASS][ITEMS][CH];
+#pragma unroll
+    for (int ps = 0; ps < MPASS; ++ps)
+#pragma unroll
+      for (int j = 0; j < ITEMS; ++j) {
+        int m, c4;
+        const bool ok = item_ok(ps, j, m, c4);
+        m = ok ? m : 0;
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+          const int sp = (k < nsplit && k != split) ? k : (split == 0 ? 1 : 0);  // a real split (not used below)
+          const int64_t rr = base0 + (int64_t)sp * a.Mv + m;
+          if (ok) {
+            ml[ps][j][k] = load_agent(reinterpret_cast<const uint64_t*>(&a.part_ml[rr * 2]));
+            o01[ps][j][k] = load_agent(reinterpret_cast<const uint64_t*>(&a.part_o[rr * DH + c4 * 4]));
+            o23[ps][j][k] = load_agent(reinterpret_cast<const uint64_t*>(&a.part_o[rr * DH + c4 * 4 + 2]));
+          }
+        }
+      }
+#pragma unroll
+    for (int ps = 0; ps < MPASS; ++ps)
+#pragma unroll
+      for (int j = 0; j < ITEMS; ++j) {
+        int m, c4;
+        if (!item_ok(ps, j, m, c4)) continue;
+        float M = kNegInf, den = 0.f;
+        f32x4 num = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+          if (k >= nsplit) break;
+          if (k == split)
+            fold(M, den, num, row_pos[m] >= 0 ? row_ms[m] : kNegInf, row_pos[m] >= 0 ? row_l[m] : 0.f, own[ps][j]);
+          else
+            fold(M, den, num, ml[ps][j][k].x, ml[ps][j][k].y,
+                 f32x4{o01[ps][j][k].x, o01[ps][j][k].y, o23[ps][j][k].x, o23[ps][j][k].y});
+        }
+        write_out(m, c4, den, num);
+      }
+    return;
+  }
+  // more splits: CH per round trip
+#pragma unroll
+  for (int ps = 0; ps < MPASS; ++ps) {
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+      int m, c4;
+      if (!item_ok(ps, j, m, c4)) continue;
+      float M = kNegInf, den = 0.f;
+      f32x4 num = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int s0 = 0; s0 < nsplit; s0 += CH) {
+        float2 ml[CH], o01[CH], o23[CH];
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+          int sp = s0 + k;
+          sp = (sp < nsplit && sp != split) ? sp : (split == 0 ? 1 : 0);  // a real split (not used below)
+          const int64_t rr = base0 + (int64_t)sp * a.Mv + m;
+          ml[k] = load_agent(reinterpret_cast<const uint64_t*>(&a.part_ml[rr * 2]));
+          o01[k] = load_agent(reinterpret_cast<const uint64_t*>(&a.part_o[rr * DH + c4 * 4]));
+          o23[k] = load_agent(reinterpret_cast<const uint64_t*>(&a.part_o[rr * DH + c4 * 4 + 2]));
+        }
+#pragma unroll
+        for (int k = 0; k < CH; ++k) {
+          const int sp = s0 + k;
+          if (sp >= nsplit) break;
+          if (sp == split)
+            fold(M, den, num, row_pos[m] >= 0 ? row_ms[m] : kNegInf, row_pos[m] >= 0 ? row_l[m] : 0.f, own[ps][j]);
+          else
+            fold(M, den, num, ml[k].x, ml[k].y, f32x4{o01[k].x, o01[k].y, o23[k].x, o23[k].y});
+        }
+      }
+      write_out(m, c4, den, num);
+    }
   }
 }
 
-// ---------------------------------------------------------------------------
 // fp32 path: one wave per workgroup, VALU dot products (exact fp32 math, the
 // 1e-5 contract).  Lane = key for Q.K, lane = head dim for P.V.
 // ---------------------------------------------------------------------------
@@ -1320,6 +1441,7 @@ struct Plan {
   int G, QL, Mv, MT, split, S, dqc;
   int ks;         // 1: key-split kernel, 0: d-sliced kernel (bf16)
   int ks_splits;  // key-split kernel, automatic splits per sequence (split == 0)
+  int ks_short;   // key-split kernel: at most 4 tiles per wave, one tile in flight per wave
 };
 
 int ilog2_exact(int v) {
@@ -1363,6 +1485,7 @@ int make_plan(int B, int H, int Hkv, int D, int block_size, int max_blocks, int 
   p->dqc = 1;
   p->ks = 0;
   p->ks_splits = 0;
+  p->ks_short = 0;
   // Kernel choice (bf16).  The key-split kernel reads every K/V byte once
   // per CU but pays about three memory round trips to merge a pair's splits;
   // the d-sliced kernel needs no cross-workgroup merge but re-reads the
@@ -1374,7 +1497,7 @@ int make_plan(int B, int H, int Hkv, int D, int block_size, int max_blocks, int 
   const int64_t ks_slots = (int64_t)cus * (8 / kKsWaves);  // resident workgroups
   const bool ks_fits = p->MT <= 3 && block_size >= 16 && max_blocks <= kMaxSplitPages &&
                        (pairs <= kMaxCounterPairs || (kv_split_tokens == 0 && pairs >= ks_slots));
-  const bool ks_wins = kv_split_tokens > 0 || pairs >= ks_slots || max_ctx >= 4096;
+  const bool ks_wins = kv_split_tokens > 0 || pairs * 4 >= ks_slots || max_ctx >= 4096;
   if (dtype == NSV_BF16 && ks_fits && ks_wins) {
     // key-split kernel: each sequence's keys evenly over about CUs / pairs
     // splits (none when the pairs alone cover the chip), or the caller's
@@ -1394,6 +1517,9 @@ int make_plan(int B, int H, int Hkv, int D, int block_size, int max_blocks, int 
       p->S = (int)((max_ctx + split - 1) / split);
     }
     if (p->S > 8192) return NSV_ERR_UNSUPPORTED;  // the merge stages 2 * S floats in LDS
+    // keys one split covers at most, and the 16-key tiles each of the 8 waves takes
+    const int64_t split_keys = p->split > 0 ? p->split : (max_ctx + p->S - 1) / p->S;
+    p->ks_short = (split_keys + 16 * kKsWaves - 1) / (16 * kKsWaves) <= 4;
     return NSV_OK;
   }
   if (dtype == NSV_BF16) {
@@ -1461,9 +1587,19 @@ constexpr int ks_stages(int MT, int DH) {
 }
 
 template <int MT>
-int launch_ks(const VerifyArgs& a, int D, dim3 grid, hipStream_t s) {
+int launch_ks(const VerifyArgs& a, int D, bool short_splits, dim3 grid, hipStream_t s) {
   if constexpr (MT <= 3) {
     constexpr int NW = kKsWaves;
+    if (short_splits) {
+      // few tiles per wave: one in flight per wave (a deeper pipeline only
+      // queues more requests at the same bandwidth; measured on MI355X at
+      // config 2: 1 stage 9.2 us, 2 stages 9.6, 4 stages 10.3 for the loads alone)
+      if (D == 128)
+        hipLaunchKernelGGL((verify_attn_ks_kernel<MT, 128, 1, NW>), grid, dim3(NW * 64), 0, s, a);
+      else
+        hipLaunchKernelGGL((verify_attn_ks_kernel<MT, 64, 1, NW>), grid, dim3(NW * 64), 0, s, a);
+      return NSV_OK;
+    }
     if (D == 128)
       hipLaunchKernelGGL((verify_attn_ks_kernel<MT, 128, ks_stages(MT, 128), NW>), grid, dim3(NW * 64), 0, s, a);
     else
@@ -1631,9 +1767,9 @@ int nsv_verify_attention(void* out, const void* q, const void* k_cache, const vo
   const dim3 grid(8 * p.S * a.P8 * p.dqc);
   if (dtype == NSV_BF16 && p.ks) {
     switch (p.MT) {
-      case 1: rc = launch_ks<1>(a, D, grid, s); break;
-      case 2: rc = launch_ks<2>(a, D, grid, s); break;
-      default: rc = launch_ks<3>(a, D, grid, s); break;
+      case 1: rc = launch_ks<1>(a, D, p.ks_short, grid, s); break;
+      case 2: rc = launch_ks<2>(a, D, p.ks_short, grid, s); break;
+      default: rc = launch_ks<3>(a, D, p.ks_short, grid, s); break;
     }
     if (rc != NSV_OK) return rc;
   } else if (dtype == NSV_BF16) {
