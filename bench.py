@@ -122,17 +122,24 @@ def measured_traffic(workload_config: int):
 def e2e_round(batches=(1, 2, 4, 8), tokens: int = 48, K: int = 8) -> dict:
     """the whole greedy n-gram verification round of a
     random-init Qwen3-0.6B (28 layers, bf16) at batch 1/2/4/8, one hipGraph
-    replay per round per batch bucket; decode tokens per second over the
-    rounds (prefill excluded, reported apart)."""
+    replay per round per batch bucket.  Reported per batch: decode tokens
+    per second over the rounds (prefill excluded), output tokens per second
+    over the whole request (prefill included, as the reference's output_tps),
+    time to first token, and the prompt tokens prefilled (the batch's
+    requests share their 1200-token document, whose full pages the prefix
+    cache serves after the first request).  Each batch runs on a fresh
+    engine, so no earlier batch warms its cache."""
     from naivllm_amd.sampling_parameters import SamplingParams
     from naivllm_amd.spec_engine.spec_llm_engine import SpecLLMEngine
 
-    eng = SpecLLMEngine(dict(spec_method="ngram", num_speculative_tokens=K, ngram_min_size=2, ngram_max_size=4,
-                             max_num_sequences=max(batches), max_model_length=1200 + 16 + tokens + 64,
-                             block_size=256, seed=0))
     sp = SamplingParams(temperature=0.0, max_tokens=tokens, ignore_eos=True)
     out = {}
     for b in batches:
+        eng = SpecLLMEngine(dict(spec_method="ngram", num_speculative_tokens=K, ngram_min_size=2, ngram_max_size=4,
+                                 max_num_sequences=max(batches), max_model_length=1200 + 16 + tokens + 64,
+                                 block_size=256, seed=0))
+        eng.generate(synth.config3_prompts(1, seed=99), SamplingParams(temperature=0.0, max_tokens=4,
+                                                                        ignore_eos=True))  # graphs captured, warm
         before = dict(eng.spec_stats)
         res = eng.generate(synth.config3_prompts(b), sp)
         m = res["metrics"]
@@ -141,17 +148,21 @@ def e2e_round(batches=(1, 2, 4, 8), tokens: int = 48, K: int = 8) -> dict:
         accepted = st["accepted_tokens"] - before["accepted_tokens"]
         out[f"b{b}"] = {
             "decode_tok_s": round(m["decode_tok_per_s"], 1),
+            "output_tok_s": round(m["output_tok_per_s"], 1),
+            "ttft_s": round(m["ttft_s"], 4),
             "decode_ms_per_round": round(1e3 * m["decode_s"] / max(m["rounds"], 1), 3),
             "rounds": m["rounds"],
             "tokens_per_round": round(m["decode_tokens"] / max(m["rounds"], 1), 3),
             "drafted": drafted,
             "accepted": accepted,
-            "prefill_s": round(m["prefill_s"], 3),
+            "prefill_tokens": m["prefill_tokens"],
+            "prefill_s": round(m["prefill_s"], 4),
             "output_tokens": m["output_tokens"],
         }
         print(f"[bench] e2e b{b}: {out[f'b{b}']}", file=sys.stderr, flush=True)
-    del eng
-    torch.cuda.empty_cache()
+        eng.exit()
+        del eng
+        torch.cuda.empty_cache()
     return out
 
 
@@ -161,37 +172,44 @@ def e2e_cascade(batches=(1, 8), tokens: int = 48, K: int = 8) -> dict:
     through the hybrid drafter (n-gram first, K = 8 GPU-resident draft
     steps otherwise), one 9-row verify forward and min(1, p_t/p_d)
     acceptance at temperature 1.0; 1200-token prefix, 48 output tokens.
-    Decode tokens per second over the rounds, one hipGraph replay per
-    round."""
+    Decode tokens per second over the rounds (one hipGraph replay per
+    round), output tokens per second over the whole request and time to
+    first token, each batch on a fresh engine."""
     from naivllm_amd.layers.qwen3 import Qwen3Config
     from naivllm_amd.sampling_parameters import SamplingParams
     from naivllm_amd.spec_engine.spec_llm_engine import SpecLLMEngine
 
-    eng = SpecLLMEngine(dict(spec_method="hybrid", num_speculative_tokens=K, ngram_min_size=2, ngram_max_size=4,
-                             model_config=Qwen3Config.qwen3_8b(), draft_model_config=Qwen3Config.qwen3_0_6b(),
-                             max_num_sequences=max(batches), max_model_length=1200 + 16 + tokens + 64,
-                             block_size=256, seed=5))
     sp = SamplingParams(temperature=1.0, max_tokens=tokens, ignore_eos=True)
     out = {}
     for b in batches:
+        eng = SpecLLMEngine(dict(spec_method="hybrid", num_speculative_tokens=K, ngram_min_size=2, ngram_max_size=4,
+                                 model_config=Qwen3Config.qwen3_8b(), draft_model_config=Qwen3Config.qwen3_0_6b(),
+                                 max_num_sequences=max(batches), max_model_length=1200 + 16 + tokens + 64,
+                                 block_size=256, seed=5))
+        eng.generate(synth.config3_prompts(1, seed=99), SamplingParams(temperature=1.0, max_tokens=4,
+                                                                        ignore_eos=True))  # graphs captured, warm
         before = dict(eng.spec_stats)
         res = eng.generate(synth.config3_prompts(b, seed=5), sp)
         m = res["metrics"]
         st = m["spec_decoding"]
         out[f"b{b}"] = {
             "decode_tok_s": round(m["decode_tok_per_s"], 1),
+            "output_tok_s": round(m["output_tok_per_s"], 1),
+            "ttft_s": round(m["ttft_s"], 4),
             "decode_ms_per_round": round(1e3 * m["decode_s"] / max(m["rounds"], 1), 3),
             "rounds": m["rounds"],
             "tokens_per_round": round(m["decode_tokens"] / max(m["rounds"], 1), 3),
             "drafted": st["drafted_tokens"] - before["drafted_tokens"],
             "accepted": st["accepted_tokens"] - before["accepted_tokens"],
             "model_fallback_seqs": st["model_fallback_seqs"] - before["model_fallback_seqs"],
-            "prefill_s": round(m["prefill_s"], 3),
+            "prefill_tokens": m["prefill_tokens"],
+            "prefill_s": round(m["prefill_s"], 4),
             "output_tokens": m["output_tokens"],
         }
         print(f"[bench] cascade b{b}: {out[f'b{b}']}", file=sys.stderr, flush=True)
-    del eng
-    torch.cuda.empty_cache()
+        eng.exit()
+        del eng
+        torch.cuda.empty_cache()
     return out
 
 

@@ -90,6 +90,7 @@ struct VerifyArgs {
   int H, Hkv, G, bs_log2, max_blocks, QL, Mv, S, split_tokens, P8, npairs;
   int dqc;           // head-dim slices per pair (d-sliced bf16 kernel)
   int ks_splits;     // key-split kernel: splits per sequence when split_tokens == 0
+  int m_base;        // fp32 kernel: first query row (of the Mv) this launch serves
 };
 
 __device__ __forceinline__ u32x4 load16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
@@ -1246,17 +1247,19 @@ __global__ __launch_bounds__(64) void verify_attn_f32_kernel(VerifyArgs a) {
   const int q0 = a.cu_seqlens_q[b];
   const int qlen = a.cu_seqlens_q[b + 1] - q0;
 
+  // local row r serves query row m = m_base + r of the pair's Mv rows
   for (int idx = lane; idx < MP * DH; idx += NSV_WAVE) {
-    const int m = idx / DH, d = idx - m * DH;
+    const int r = idx / DH, d = idx - r * DH;
+    const int m = a.m_base + r;
     const int g = m / a.QL, t = m - g * a.QL;
     const bool ok = (m < a.Mv) && (t < qlen);
-    q_s[m][d] = ok ? ((const float*)a.q)[((int64_t)(q0 + t) * a.H + hk * a.G + g) * DH + d] : 0.f;
+    q_s[r][d] = ok ? ((const float*)a.q)[((int64_t)(q0 + t) * a.H + hk * a.G + g) * DH + d] : 0.f;
   }
   if (lane < MP) {
-    const int m = lane;
+    const int m = a.m_base + lane;
     const int g = m / a.QL, t = m - g * a.QL;
     const bool ok = (m < a.Mv) && (t < qlen);
-    pos_s[m] = ok ? (int)a.positions[q0 + t] : -1;
+    pos_s[lane] = ok ? (int)a.positions[q0 + t] : -1;
   }
   __syncthreads();
 
@@ -1333,25 +1336,26 @@ __global__ __launch_bounds__(64) void verify_attn_f32_kernel(VerifyArgs a) {
   if (nsplit == 1) {
     float* out = (float*)a.out;
 #pragma unroll
-    for (int m = 0; m < MP; ++m) {
+    for (int r = 0; r < MP; ++r) {
+      const int m = a.m_base + r;
       const int g = m / a.QL, t = m - g * a.QL;
       if (m >= a.Mv || t >= qlen) continue;
 #pragma unroll
       for (int e = 0; e < E; ++e)
         out[((int64_t)(q0 + t) * a.H + hk * a.G + g) * DH + lane + 64 * e] =
-            l_run[m] > 0.f ? acc[m][e] / l_run[m] : 0.f;
+            l_run[r] > 0.f ? acc[r][e] / l_run[r] : 0.f;
     }
     return;
   }
-  const int64_t base = ((int64_t)pair * a.S + split) * a.Mv;
+  const int64_t base = ((int64_t)pair * a.S + split) * a.Mv + a.m_base;
 #pragma unroll
-  for (int m = 0; m < MP; ++m) {
-    if (m >= a.Mv) continue;
+  for (int r = 0; r < MP; ++r) {
+    if (a.m_base + r >= a.Mv) continue;
 #pragma unroll
-    for (int e = 0; e < E; ++e) a.part_o[(base + m) * DH + lane + 64 * e] = acc[m][e];
+    for (int e = 0; e < E; ++e) a.part_o[(base + r) * DH + lane + 64 * e] = acc[r][e];
     if (lane == 0) {
-      a.part_ml[(base + m) * 2 + 0] = m_run[m];
-      a.part_ml[(base + m) * 2 + 1] = l_run[m];
+      a.part_ml[(base + r) * 2 + 0] = m_run[r];
+      a.part_ml[(base + r) * 2 + 1] = l_run[r];
     }
   }
 }
@@ -1631,12 +1635,25 @@ int launch_bf16(const VerifyArgs& a, int D, dim3 grid, hipStream_t s) {
   return NSV_ERR_UNSUPPORTED;
 }
 
+// fp32: at most two 16-row tiles per launch; more query rows per pair run
+// as further launches over the next 32 rows (the single-launch form for 64
+// rows, 256 VGPRs + 254 AGPRs of row state per lane, returned wrong rows on
+// MI355X; two launches read the pair's K/V twice, which the 1e-5 path can
+// afford).
 template <int MT>
 void launch_f32(const VerifyArgs& a, int D, dim3 grid, hipStream_t s) {
-  if (D == 128)
-    hipLaunchKernelGGL((verify_attn_f32_kernel<MT, 128>), grid, dim3(64), 0, s, a);
-  else
-    hipLaunchKernelGGL((verify_attn_f32_kernel<MT, 64>), grid, dim3(64), 0, s, a);
+  if constexpr (MT <= 2) {
+    if (D == 128)
+      hipLaunchKernelGGL((verify_attn_f32_kernel<MT, 128>), grid, dim3(64), 0, s, a);
+    else
+      hipLaunchKernelGGL((verify_attn_f32_kernel<MT, 64>), grid, dim3(64), 0, s, a);
+  } else {
+    VerifyArgs b = a;
+    b.m_base = 0;
+    launch_f32<2>(b, D, grid, s);
+    b.m_base = 32;
+    launch_f32<MT - 2>(b, D, grid, s);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1762,6 +1779,7 @@ int nsv_verify_attention(void* out, const void* q, const void* k_cache, const vo
   a.P8 = (B * Hkv + 7) / 8;
   a.dqc = p.dqc;
   a.ks_splits = p.ks_splits;
+  a.m_base = 0;
 
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid(8 * p.S * a.P8 * p.dqc);

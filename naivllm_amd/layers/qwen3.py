@@ -158,6 +158,44 @@ FUSED_ROWS_WIDE = 12  # hidden size above 2048
 LM_HEAD_ROWS = 16
 
 
+def prefill_metadata(token_lists, starts, tables, block_size: int, q_block: int, device):
+    """Rows of one prefill forward over several sequences' new tokens.
+
+    Sequence i contributes its tokens starts[i] .. len(token_lists[i]) - 1 at
+    their positions (the pages before starts[i] already hold their KV: a
+    cached prefix).  Its rows are cut into causal blocks of q_block rows;
+    each block is one entry of the verify attention's batch, whose context
+    ends at the block's last position and whose block-table row is the
+    sequence's, so every row attends exactly the keys 0 .. its position.
+    Returns (input_ids, positions, slot_mapping, block_tables, context_lens,
+    cu_seqlens_q, last_rows) on ``device``; last_rows[i] is the row of
+    sequence i's last token."""
+    import numpy as np
+
+    ids, pos, slots, ctx, cu, bt_rows, last = [], [], [], [], [0], [], []
+    width = max(len(t) for t in tables)
+    for toks, start, table in zip(token_lists, starts, tables):
+        n = len(toks)
+        if not 0 <= start < n:
+            raise ValueError(f"prefill start {start} outside a {n}-token sequence")
+        p = np.arange(start, n, dtype=np.int64)
+        page = np.asarray(table, dtype=np.int64)[p // block_size]
+        ids.append(np.asarray(toks[start:], dtype=np.int64))
+        pos.append(p)
+        slots.append(page * block_size + p % block_size)
+        row = np.full(width, -1, dtype=np.int32)
+        row[:len(table)] = table
+        for b0 in range(start, n, q_block):
+            b1 = min(n, b0 + q_block)
+            ctx.append(b1)
+            cu.append(cu[-1] + (b1 - b0))
+            bt_rows.append(row)
+        last.append(cu[-1] - 1)
+    t = lambda x, dt: torch.from_numpy(np.ascontiguousarray(x, dtype=dt)).to(device)  # noqa: E731
+    return (t(np.concatenate(ids), np.int64), t(np.concatenate(pos), np.int64), t(np.concatenate(slots), np.int64),
+            t(np.stack(bt_rows), np.int32), t(ctx, np.int64), t(cu, np.int32), t(last, np.int64))
+
+
 def fused_rows(hidden_size: int) -> int:
     return FUSED_ROWS if hidden_size <= 2048 else FUSED_ROWS_WIDE
 
@@ -197,6 +235,20 @@ class Qwen3Verify:
         self.v_caches: list[torch.Tensor] = []
         self.block_size = 0
 
+    def prefill_q_block(self) -> int:
+        """Query rows per causal block of a prefill: the verify kernel serves
+        up to 64 (GQA group x rows) per (sequence, kv head)."""
+        return 64 // (self.cfg.num_heads // self.cfg.num_kv_heads)
+
+    @torch.inference_mode()
+    def prefill(self, token_lists, starts, tables) -> torch.Tensor:
+        """One forward over the new tokens of several sequences (see
+        prefill_metadata): their K/V land in the paged cache, and the logits
+        of each sequence's last token come back, [len(token_lists), vocab]."""
+        ids, pos, slots, bt, ctx, cu, last = prefill_metadata(token_lists, starts, tables, self.block_size,
+                                                              self.prefill_q_block(), self.device)
+        return self.forward(ids, pos, slots, bt, ctx, cu, self.prefill_q_block(), logits_rows=last)
+
     def allocate_kv_cache(self, num_blocks: int, block_size: int) -> None:
         """One [num_blocks, block_size, Hkv, D] K and V pool per layer
         (engine/model_runner.py:244-279 keeps one [2, L, ...] tensor)."""
@@ -208,10 +260,12 @@ class Qwen3Verify:
 
     def forward(self, input_ids: torch.Tensor, positions: torch.Tensor, slot_mapping: torch.Tensor,
                 block_tables: torch.Tensor, context_lens: torch.Tensor, cu_seqlens_q: torch.Tensor,
-                max_q_len: int, logits_out: torch.Tensor | None = None) -> torch.Tensor:
+                max_q_len: int, logits_out: torch.Tensor | None = None,
+                logits_rows: torch.Tensor | None = None) -> torch.Tensor:
         """Verify forward over T = sum of per-sequence query rows.  Rows at
         position -1 are inert padding (no KV store, zero attention output).
-        Returns logits [T, vocab] (written into logits_out when given)."""
+        Returns logits [T, vocab] (written into logits_out when given), or
+        only the rows ``logits_rows`` indexes (the prefill's last rows)."""
         if self.dtype != torch.bfloat16:
             raise ValueError("the fused forward kernels are bf16")
         cfg = self.cfg
@@ -266,6 +320,9 @@ class Qwen3Verify:
                 silu_mul(F.linear(h, L["gate_up"]), act)
                 x = F.linear(act, L["down"])
             rms_norm(x, self.norm, eps, h, residual=resid)
+        if logits_rows is not None:
+            h = h.index_select(0, logits_rows)
+            T = h.shape[0]
         # the LM head: the few-row kernel up to LM_HEAD_ROWS rows (it streams the
         # vocabulary's weight rows faster there), hipBLASLt's large tiles beyond
         if T <= LM_HEAD_ROWS:

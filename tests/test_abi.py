@@ -64,9 +64,19 @@ def test_workspace_size_matches_split_plan():
     rows = 8 * 8 * 12 * 18
     cnt = 65536
     assert h.nsv_verify_attention_workspace_size(8, 16, 8, 128, 256, 6, 9, 1, 128) == cnt + pad(rows * 8) + rows * 512
-    # automatic plan for config 2 (6-page tables): the d-sliced kernel, 64 (sequence, kv-head)
-    # pairs x 4 head-dim slices fill the chip without key splits, so no workspace
-    assert h.nsv_verify_attention_workspace_size(8, 16, 8, 128, 256, 6, 9, 1, 0) == 0
+    # automatic plan for config 2 (6-page tables): the key-split kernel, 64 (sequence, kv-head)
+    # pairs x 4 key splits fill the 256 CUs a host without a GPU assumes
+    rows = 8 * 8 * 4 * 18
+    assert h.nsv_verify_attention_workspace_size(8, 16, 8, 128, 256, 6, 9, 1, 0) == cnt + pad(rows * 8) + rows * 512
+    # 4 sequences: 32 pairs x 4 key splits leave half the CUs idle, so the d-sliced kernel
+    # (4 head-dim slices, 2 key splits merged by a second kernel) keeps the shape
+    import ctypes
+    kind, splits = ctypes.c_int(), ctypes.c_int()
+    assert h.nsv_verify_attention_plan(4, 16, 8, 128, 256, 6, 9, 1, 0, 256, ctypes.addressof(kind),
+                                       ctypes.addressof(splits)) == 0
+    assert (kind.value, splits.value) == (0, 2)
+    rows = 4 * 8 * 2 * 18
+    assert h.nsv_verify_attention_workspace_size(4, 16, 8, 128, 256, 6, 9, 1, 0) == cnt + pad(rows * 8) + rows * 512
     # 16-page tables (4096 keys): the key-split kernel, 4 splits per sequence for 64 pairs on
     # the 256 CUs a host without a GPU assumes
     rows = 8 * 8 * 4 * 18

@@ -83,7 +83,7 @@ def _load_round(eng, r, prompts, sp):
         s = Sequence(p, sp)
         eng.block_manager.allocate(s)
         eng.block_manager.ensure_capacity(s, len(p) + sp.max_tokens + eng.num_speculative_tokens + 1)
-        first = eng._prefill(s)
+        first = eng._prefill([s])[0]
         h = list(p) + [first]
         hists.append(h)
         r.history[b].zero_()

@@ -69,7 +69,7 @@ def _load(eng, r, hists, max_tokens=100, temps=None):
         s = Sequence(h, SamplingParams(temperature=temps[b] if temps else 0.0))
         eng.block_manager.allocate(s)
         eng.block_manager.ensure_capacity(s, len(h) + 64)
-        eng._prefill(s)
+        eng._prefill([s])
         r.history[b].zero_()
         r.history[b, :len(h)] = torch.tensor(h, dtype=torch.int32, device="cuda")
         r.hist_len[b] = len(h)

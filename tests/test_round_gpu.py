@@ -90,7 +90,7 @@ def test_one_round_matches_host_restatement():
         s = Sequence(h)
         eng.block_manager.allocate(s)
         eng.block_manager.ensure_capacity(s, len(h) + 64)
-        eng._prefill(s)
+        eng._prefill([s])
         r.history[b, :len(h)] = torch.tensor(h, dtype=torch.int32, device="cuda")
         r.hist_len[b] = len(h)
         r.prompt_len[b] = len(h) - 2
