@@ -213,43 +213,212 @@ def e2e_cascade(batches=(1, 8), tokens: int = 48, K: int = 8) -> dict:
     return out
 
 
-def cpu_baseline(seconds: float) -> dict:
-    """The torch-on-CPU restatement of the same verify-attention call
-    (config 2 shape, one layer), timed on this host's cores."""
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown CPU"
+
+
+def _median_seconds(fn, warmup: int = 5, reps: int = 20) -> float:
+    for _ in range(warmup):
+        fn()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times))
+
+
+def cpu_baseline() -> dict:
+    """BASELINE config 1 on the host's cores (the torch-CPU restatement of
+    the reference's path, oracle/torch_cpu.py): one verify-attention call
+    (b1 fp32, 16Q/8KV, d 128, L = 1248 in 5 pages of a seeded-permuted
+    64-page pool, 9 query rows; layers/attention.py:328-363) plus the greedy
+    acceptance of 8 drafts over [9, 151936] fp32 logits ~ N(0, 2^2) whose
+    first 5 drafts are the argmax (spec_llm_engine.py:224-227,
+    rejection_sampler.py:25-36).  5 warm-up reps, then the median of 20,
+    with every host thread and with one.  Also the config-2 attention call
+    (b8 bf16), the GPU metric's workload, with every thread."""
     from oracle import torch_cpu
 
+    H, Hkv, D, bs, R, V = 16, 8, 128, 256, 9, 151936
+    g = torch.Generator().manual_seed(1)
+    kc = torch.randn(64, bs, Hkv, D, generator=g)
+    vc = torch.randn(64, bs, Hkv, D, generator=g)
+    q = torch.randn(R, H, D, generator=g)
+    bt = torch.randperm(64, generator=g)[:5].to(torch.int32)[None]
+    L = 1248
+    args1 = (q, kc, vc, bt, torch.tensor([L]), torch.tensor([0, R], dtype=torch.int32), torch.arange(L - R, L),
+             1 / np.sqrt(D), H, Hkv)
+    logits = torch.randn(R, V, generator=g) * 2.0
+    am = logits.argmax(-1).tolist()
+    drafts = [am[:5] + [int(x) for x in torch.randint(0, V, (3,), generator=g)]]
+    accepted = torch_cpu.greedy_accept(drafts, logits, R)
+    attn_bytes = L * Hkv * D * 2 * 4 + 2 * R * H * D * 4 + 4 * 5 + 8 + 8 + 8 * R
+    accept_bytes = R * V * 4
+    step = lambda: (torch_cpu.paged_verify_attention(*args1), torch_cpu.greedy_accept(drafts, logits, R))  # noqa: E731
     threads = os.cpu_count() or 1
+    out = {"unit": "GB/s", "kind": "port", "cpu": cpu_model()}
+    for n in (threads, 1):
+        torch.set_num_threads(n)
+        sec = _median_seconds(step)
+        key = "all_threads" if n == threads else "one_thread"
+        out[key] = {"threads": n, "median_ms": round(sec * 1e3, 3),
+                    "GBs": round((attn_bytes + accept_bytes) / sec / 1e9, 3)}
     torch.set_num_threads(threads)
-    vb_ctx = synth.config2_ctx_lens(2, 8)
-    B, H, Hkv, D, bs, rows = 8, 16, 8, 128, 256, 9
-    pages = [(c + bs - 1) // bs for c in vb_ctx]
-    g = torch.Generator().manual_seed(2)
+    out["value"] = out["all_threads"]["GBs"]
+    out["cores"] = threads
+    out["sample"] = (f"BASELINE config 1: one verify-attention call (b1 fp32, L=1248, 16Q/8KV, d128) + greedy "
+                     f"acceptance over [9, 151936] fp32 logits ({len(accepted[0])} tokens accepted), median of 20 "
+                     f"after 5 warm-ups on {out['cpu']}; {attn_bytes + accept_bytes} algorithmic bytes per step")
+    # config 2's attention call (the GPU metric's workload), every thread
+    ctx2 = synth.config2_ctx_lens(2, 8)
+    pages = [(c + bs - 1) // bs for c in ctx2]
+    g2 = torch.Generator().manual_seed(2)
     nb = sum(pages) + 4
-    kc = torch.randn(nb, bs, Hkv, D, generator=g).to(torch.bfloat16)
-    vc = torch.randn(nb, bs, Hkv, D, generator=g).to(torch.bfloat16)
-    q = torch.randn(B * rows, H, D, generator=g).to(torch.bfloat16)
-    bt = torch.full((B, max(pages)), -1, dtype=torch.int32)
+    kc2 = torch.randn(nb, bs, Hkv, D, generator=g2).to(torch.bfloat16)
+    vc2 = torch.randn(nb, bs, Hkv, D, generator=g2).to(torch.bfloat16)
+    q2 = torch.randn(8 * R, H, D, generator=g2).to(torch.bfloat16)
+    bt2 = torch.full((8, max(pages)), -1, dtype=torch.int32)
     off = 0
-    for b in range(B):
-        bt[b, :pages[b]] = torch.arange(off, off + pages[b], dtype=torch.int32)
+    for b in range(8):
+        bt2[b, :pages[b]] = torch.arange(off, off + pages[b], dtype=torch.int32)
         off += pages[b]
-    ctx = torch.tensor(vb_ctx)
-    cu = torch.arange(0, B * rows + 1, rows, dtype=torch.int32)
-    pos = torch.cat([torch.arange(c - rows, c) for c in vb_ctx])
-    args = (q, kc, vc, bt, ctx, cu, pos, 1 / np.sqrt(D), H, Hkv)
-    torch_cpu.paged_verify_attention(*args)  # warm
-    n, t0 = 0, time.perf_counter()
-    while True:
-        torch_cpu.paged_verify_attention(*args)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= seconds:
-            break
-    nbytes = algorithmic_bytes(vb_ctx, B * rows, H, Hkv, D, 2, max(pages))
-    return {"value": round(nbytes * n / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{n} calls of the config-2 verify-attention (b8 bf16, one layer) in {el:.1f} s, "
-                      f"torch CPU restatement of layers/attention.py:328-363 on {platform.processor() or 'host'} "
-                      f"with {threads} threads"}
+    args2 = (q2, kc2, vc2, bt2, torch.tensor(ctx2), torch.arange(0, 8 * R + 1, R, dtype=torch.int32),
+             torch.cat([torch.arange(c - R, c) for c in ctx2]), 1 / np.sqrt(D), H, Hkv)
+    sec = _median_seconds(lambda: torch_cpu.paged_verify_attention(*args2))
+    nbytes = algorithmic_bytes(ctx2, 8 * R, H, Hkv, D, 2, max(pages))
+    out["config2_attention"] = {"threads": threads, "median_ms": round(sec * 1e3, 3),
+                                "GBs": round(nbytes / sec / 1e9, 3)}
+    return out
+
+
+def _graph_us(step, calls_per_step: int, steps: int = 50, warmup: int = 5) -> float:
+    """Average duration of one call: ``step`` (calls_per_step launches on
+    the current stream) is captured as a hipGraph and replayed; HIP events
+    on that stream bracket the timed replays."""
+    for _ in range(2):
+        step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (steps * calls_per_step)
+
+
+def ceilings(wl: "Workload") -> dict:
+    """Load-only ceilings of the metric's workload, timed like the metric:
+    the verify-attention K/V bytes read in the key-split kernel's access
+    pattern with nothing computed (nsv_verify_attention_load_floor, same
+    28 rotating pools, the plan's splits), and a contiguous read of the
+    same byte count from 28 rotating flat buffers (nsv_stream_read, 1024
+    workgroups)."""
+    from naivllm_amd import _lib
+    from naivllm_amd.layers.attention import verify_attention_plan
+
+    h = _lib.lib()
+    dev = wl.q.device
+    kind, splits = verify_attention_plan(wl.B, wl.H, wl.Hkv, wl.D, wl.bs, wl.max_blocks, wl.rows, torch.bfloat16)
+    splits = splits if kind == "key-split" else 4
+    sink = torch.zeros(65536, dtype=torch.int32, device=dev)
+    kv_bytes = sum(wl.ctx) * wl.Hkv * wl.D * 2 * 2
+
+    def floor_step():
+        s = torch.cuda.current_stream().cuda_stream
+        for layer in range(wl.layers):
+            rc = h.nsv_verify_attention_load_floor(wl.k_caches[layer].data_ptr(), wl.v_caches[layer].data_ptr(),
+                                                  wl.block_tables.data_ptr(), wl.context_lens.data_ptr(), wl.B,
+                                                  wl.Hkv, wl.D, wl.bs, wl.max_blocks, splits, sink.data_ptr(), s)
+            _lib.check(rc, "load floor")
+    floor_us = _graph_us(floor_step, wl.layers)
+    flat = [torch.ones(kv_bytes, dtype=torch.uint8, device=dev) for _ in range(wl.layers)]
+
+    def stream_step():
+        s = torch.cuda.current_stream().cuda_stream
+        for layer in range(wl.layers):
+            _lib.check(h.nsv_stream_read(flat[layer].data_ptr(), kv_bytes, 1024, sink.data_ptr(), s), "stream")
+    stream_us = _graph_us(stream_step, wl.layers)
+    del flat
+    torch.cuda.empty_cache()
+    return {"kv_bytes": kv_bytes, "splits": splits,
+            "load_floor_us": round(floor_us, 3), "load_floor_GBs": round(kv_bytes / floor_us / 1e3, 1),
+            "stream_us": round(stream_us, 3), "stream_GBs": round(kv_bytes / stream_us / 1e3, 1)}
+
+
+def rejection_sampling(seed: int = 2, sets: int = 8) -> dict:
+    """BASELINE config 2's rejection sampling on the GPU: B = 8, K = 8 model
+    drafts per sequence over V = 151936, bf16 draft logits ~ N(0, 2^2) and
+    target = draft + 0.5 N(0, 1) (the 9th target row its own N(0, 2^2)),
+    drafts sampled from the draft distribution, seeded uniforms and
+    exponential noise, T = 1 (nsv_accept_stochastic: min(1, p_t/p_d)
+    acceptance with residual resampling).  ``sets`` distinct input sets
+    (8 x 51 MB, past the 256 MB Infinity Cache) rotate through a hipGraph
+    of one call per set.  Also the greedy acceptance (argmax walk) of the
+    same target rows.  Algorithmic bytes per call: the target rows
+    (72 x V x 2), the draft rows (64 x V x 2), each sequence's noise row
+    (V x 2), uniforms, drafts and outputs."""
+    from naivllm_amd.spec_engine.rejection_sampler import accept_greedy, accept_stochastic
+
+    B, K, V = 8, 8, 151936
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(seed)
+    ins = []
+    for _ in range(sets):
+        draft = (torch.randn(B, K, V, generator=g, device=dev) * 2.0)
+        target = torch.empty(B, K + 1, V, device=dev)
+        target[:, :K] = draft + 0.5 * torch.randn(B, K, V, generator=g, device=dev)
+        target[:, K] = torch.randn(B, V, generator=g, device=dev) * 2.0
+        pd = torch.softmax(draft, -1)
+        drafts = torch.multinomial(pd.view(-1, V), 1, generator=g).view(B, K).to(torch.int32)
+        ins.append(dict(target=target.to(torch.bfloat16).view(B * (K + 1), V).contiguous(),
+                        draft=draft.to(torch.bfloat16).view(B * K, V).contiguous(), drafts=drafts,
+                        uniforms=torch.rand(B, K, generator=g, device=dev),
+                        noise=torch.empty(B, V, device=dev).exponential_(1, generator=g).to(torch.bfloat16)))
+        del draft, target, pd
+    nd = torch.full((B,), K, dtype=torch.int32, device=dev)
+    temp = torch.ones(B, dtype=torch.float32, device=dev)
+    out_t = torch.empty(B, K + 1, dtype=torch.int32, device=dev)
+    out_n = torch.empty(B, dtype=torch.int32, device=dev)
+
+    def stoch_step():
+        for x in ins:
+            accept_stochastic(x["target"], x["drafts"], nd, temp, x["noise"], uniforms=x["uniforms"],
+                              draft_logits=x["draft"], target_seq_stride=K + 1, draft_seq_stride=K,
+                              draft_row_stride=1, out_tokens=out_t, out_len=out_n)
+
+    def greedy_step():
+        for x in ins:
+            accept_greedy(x["target"], x["drafts"], nd, K + 1, out_tokens=out_t, out_len=out_n)
+
+    st_us = _graph_us(stoch_step, sets, steps=20)
+    gr_us = _graph_us(greedy_step, sets, steps=20)
+    st_bytes = B * (K + 1) * V * 2 + B * K * V * 2 + B * V * 2 + B * K * 4 * 2 + B * 4 + B * (K + 2) * 4 + B * 4
+    gr_bytes = B * (K + 1) * V * 2 + B * K * 4 + B * 4 + B * (K + 2) * 4
+    del ins
+    torch.cuda.empty_cache()
+    return {"stochastic": {"us_per_call": round(st_us, 3), "bytes_per_call": st_bytes,
+                           "GBs": round(st_bytes / st_us / 1e3, 1),
+                           "frac": round(st_bytes / st_us / 1e3 / HBM_PEAK_GBS, 4)},
+            "greedy": {"us_per_call": round(gr_us, 3), "bytes_per_call": gr_bytes,
+                       "GBs": round(gr_bytes / gr_us / 1e3, 1),
+                       "frac": round(gr_bytes / gr_us / 1e3 / HBM_PEAK_GBS, 4)},
+            "workload": "config 2 acceptance: B=8, K=8 model drafts, V=151936, bf16 logits, T=1, "
+                        f"{sets} rotating input sets"}
 
 
 def copy_probe(mib: int) -> None:
@@ -273,8 +442,11 @@ def main():
     ap.add_argument("--config", type=int, default=2)
     ap.add_argument("--layers", type=int, default=28)
     ap.add_argument("--split", type=int, default=0, help="keys per workgroup split (0 = automatic)")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--ceiling", action="store_true",
+                    help="run only the load-only ceilings of the workload (for a rocprofv3 trace) and exit")
+    ap.add_argument("--accept", action="store_true",
+                    help="run only the config-2 acceptance timings (for a rocprofv3 trace) and exit")
     ap.add_argument("--no-e2e", action="store_true", help="skip the config-3 end-to-end round measurement")
     ap.add_argument("--no-cascade", action="store_true",
                     help="skip the config-5 measurement (Qwen3-0.6B drafter feeding Qwen3-8B, hybrid, T=1)")
@@ -294,8 +466,14 @@ def main():
         raise SystemExit("bench.py needs a GPU")
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.accept:
+        print(json.dumps({"rejection_sampling": rejection_sampling()}), flush=True)
+        return
     wl = Workload(args.config, args.layers, args.seed, dev)
     print(f"[bench] workload: {wl.name}; ctx={wl.ctx}", file=sys.stderr, flush=True)
+    if args.ceiling:
+        print(json.dumps({"ceiling": ceilings(wl)}), flush=True)
+        return
     # One step (every layer's verify-attention call) is captured as a hipGraph
     # and replayed, as the verify round runs it: the timed region holds GPU
     # work only, not Python launch overhead.
@@ -325,9 +503,15 @@ def main():
     print(f"[bench] {calls} calls, {us_per_call:.2f} us/call, {gbs:.1f} GB/s, {tflops:.1f} TFLOP/s",
           file=sys.stderr, flush=True)
 
+    ceil = ceilings(wl)
+    print(f"[bench] ceilings: {ceil}", file=sys.stderr, flush=True)
+    wl.k_caches, wl.v_caches = [], []  # free the pools before the other measurements
+    torch.cuda.empty_cache()
+    accept = rejection_sampling()
+    print(f"[bench] acceptance: {accept}", file=sys.stderr, flush=True)
     e2e = None if args.no_e2e else e2e_round()
     cascade = None if (args.no_e2e or args.no_cascade) else e2e_cascade()
-    cpu = None if args.no_cpu else cpu_baseline(args.cpu_seconds)
+    cpu = None if args.no_cpu else cpu_baseline()
     line = {
         "metric": METRIC,
         "value": round(gbs, 2),
@@ -351,6 +535,9 @@ def main():
                      "traffic_source": "profiles/verify_attn_config2_traffic.md (rocprofv3 FETCH_SIZE x2 + WRITE_SIZE x1)",
                      "bytes_per_call": wl.bytes, "mfma_tflops": round(tflops, 2),
                      "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 5)},
+        "ceiling": dict(ceil, kernel_vs_load_floor=round(ceil["load_floor_us"] / us_per_call, 4),
+                        kernel_vs_stream=round(ceil["stream_us"] / us_per_call, 4)),
+        "rejection_sampling": accept,
         "accepted_tok_s": e2e,
         "cascade_tok_s": cascade,
         "cpu_baseline": cpu,

@@ -85,6 +85,25 @@ int nsv_verify_attention(void* out, const void* q, const void* k_cache,
                          size_t workspace_bytes, void* stream);
 
 /*
+ * Load-only measurement kernels, no reference counterpart (the ceilings
+ * against which bench.py --ceiling reads the verify-attention kernels).
+ * nsv_verify_attention_load_floor reads exactly the K/V bytes of a bf16,
+ * D = 128 verify-attention call over `splits` key splits per (sequence, kv
+ * head), in the key-split kernel's access pattern, and computes nothing;
+ * nsv_stream_read reads `bytes` (a multiple of 16) of contiguous memory in
+ * `workgroups` equal chunks.  `sink` is a device buffer of one uint32 per
+ * workgroup that is written only for an improbable checksum.
+ */
+int nsv_verify_attention_load_floor(const void* k_cache, const void* v_cache,
+                                    const int32_t* block_tables,
+                                    const int64_t* context_lens, int B,
+                                    int Hkv, int D, int block_size,
+                                    int max_blocks, int splits, void* sink,
+                                    void* stream);
+int nsv_stream_read(const void* buf, size_t bytes, int workgroups,
+                    void* sink, void* stream);
+
+/*
  * Allocation-free variant of nsv_verify_attention: same arguments and
  * results, minus the workspace.  No reference counterpart: it is for callers
  * that cannot allocate device memory (code under hipGraph capture, tight

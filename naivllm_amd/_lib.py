@@ -37,6 +37,8 @@ SIGNATURES: dict[str, tuple] = {
     "nsv_verify_attention_noalloc": (
         _c_int,
         [_c_vp] * 8 + [_c_f32] + [_c_int] * 10 + [_c_vp]),
+    "nsv_verify_attention_load_floor": (_c_int, [_c_vp] * 4 + [_c_int] * 6 + [_c_vp, _c_vp]),
+    "nsv_stream_read": (_c_int, [_c_vp, _c_size, _c_int, _c_vp, _c_vp]),
     "nsv_store_kv": (_c_int, [_c_vp] * 5 + [_c_int] * 5 + [_c_vp]),
     "nsv_accept_workspace_size": (_c_size, [_c_int] * 5),
     "nsv_accept_greedy": (

@@ -1657,6 +1657,75 @@ void launch_f32(const VerifyArgs& a, int D, dim3 grid, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------
+// Load-only measurement kernels (the ceilings bench.py --ceiling reports).
+// ---------------------------------------------------------------------------
+// attn_load_floor_kernel reads exactly the K/V bytes of the key-split kernel,
+// in its access pattern: workgroup = (pair, key split) with every split of a
+// pair on one XCD, the block-table row staged in LDS first, then each of the
+// 8 waves streams its interleaved 16-key tiles (K and V rows of one kv head,
+// whole 256-byte rows, 4 + 4 loads of 16 bytes per lane) with one tile in
+// flight.  Nothing is computed; the loaded words are folded into one value
+// written only if it equals a constant no input produces in practice.
+__global__ __launch_bounds__(512) void attn_load_floor_kernel(VerifyArgs a, uint32_t* sink) {
+  const int wg = blockIdx.x;
+  const int yy = wg >> 3;
+  const int pair = (yy % a.P8) * 8 + (wg & 7);
+  const int split = yy / a.P8;
+  if (pair >= a.npairs) return;
+  const int b = pair / a.Hkv, hk = pair - b * a.Hkv;
+  __shared__ int pages[kMaxSplitPages];
+  for (int j = threadIdx.x; j < a.max_blocks; j += 512) pages[j] = a.block_tables[(int64_t)b * a.max_blocks + j];
+  const int ctx = context_len(a, b);
+  __syncthreads();
+  const int nsplit = num_splits(a, ctx);
+  if (split >= nsplit) return;
+  const int len = split_len(a, ctx);
+  const int kb = split * len, ke = min(ctx, kb + len);
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int ntiles = (ke - kb + 15) / 16;
+  const unsigned row_bytes = (unsigned)a.Hkv * 256;
+  const int bs_mask = (1 << a.bs_log2) - 1;
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  for (int t = w; t < ntiles; t += 8) {
+    const int n0 = kb + t * 16;
+    const int pg = pages[n0 >> a.bs_log2];
+    if (pg < 0) continue;
+    const size_t base = ((size_t)pg << a.bs_log2) * row_bytes + (size_t)hk * 256 + (lane & 15) * 16;
+    u32x4 kv[8];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int key = ((n0 & bs_mask) + j * 4 + (lane >> 4));
+      kv[j] = load16((const char*)a.k_cache + base + (size_t)key * row_bytes);
+      kv[4 + j] = load16((const char*)a.v_cache + base + (size_t)key * row_bytes);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc ^= kv[j];
+  }
+  const uint32_t x = acc.x ^ acc.y ^ acc.z ^ acc.w;
+  if (x == 0x9e3779b9u) sink[blockIdx.x] = x;
+}
+
+// Contiguous read of `bytes` in equal per-workgroup chunks, 4 loads of 16
+// bytes per lane in flight: the streaming ceiling at a given size.
+__global__ __launch_bounds__(512) void stream_read_kernel(const char* buf, size_t per, size_t bytes, uint32_t* sink) {
+  const size_t beg = (size_t)blockIdx.x * per;
+  const size_t end = beg + per < bytes ? beg + per : bytes;
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  constexpr size_t step = 512 * 16;
+  size_t off = beg + threadIdx.x * 16;
+  for (; off + 3 * step + 16 <= end; off += 4 * step) {
+    u32x4 t[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) t[u] = load16(buf + off + u * step);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc ^= t[u];
+  }
+  for (; off + 16 <= end; off += step) acc ^= load16(buf + off);
+  const uint32_t x = acc.x ^ acc.y ^ acc.z ^ acc.w;
+  if (x == 0x9e3779b9u) sink[blockIdx.x] = x;
+}
+
+// ---------------------------------------------------------------------------
 // Scratch of the allocation-free entry point (nsv_verify_attention_noalloc).
 // ---------------------------------------------------------------------------
 // A fixed device array holds what the caller's workspace holds otherwise:
@@ -1816,6 +1885,39 @@ int nsv_verify_attention(void* out, const void* q, const void* k_cache, const vo
     if (D == 128) hipLaunchKernelGGL((verify_merge_kernel<float, 2>), mgrid, dim3(256), 0, s, a);
     else hipLaunchKernelGGL((verify_merge_kernel<float, 1>), mgrid, dim3(256), 0, s, a);
   }
+  return nsv_launch_status();
+}
+
+int nsv_verify_attention_load_floor(const void* k_cache, const void* v_cache, const int32_t* block_tables,
+                                    const int64_t* context_lens, int B, int Hkv, int D, int block_size,
+                                    int max_blocks, int splits, void* sink, void* stream) {
+  if (B < 0 || Hkv <= 0 || max_blocks <= 0 || splits <= 0 || splits > 64) return NSV_ERR_ARG;
+  if (D != 128 || ilog2_exact(block_size) < 4 || max_blocks > kMaxSplitPages) return NSV_ERR_UNSUPPORTED;
+  if (B == 0) return NSV_OK;
+  if (!k_cache || !v_cache || !block_tables || !context_lens || !sink) return NSV_ERR_ARG;
+  VerifyArgs a{};
+  a.k_cache = k_cache;
+  a.v_cache = v_cache;
+  a.block_tables = block_tables;
+  a.context_lens = context_lens;
+  a.Hkv = Hkv;
+  a.bs_log2 = ilog2_exact(block_size);
+  a.max_blocks = max_blocks;
+  a.npairs = B * Hkv;
+  a.P8 = (B * Hkv + 7) / 8;
+  a.split_tokens = 0;
+  a.ks_splits = splits;
+  hipLaunchKernelGGL(attn_load_floor_kernel, dim3(8 * splits * a.P8), dim3(512), 0, (hipStream_t)stream, a,
+                     (uint32_t*)sink);
+  return nsv_launch_status();
+}
+
+int nsv_stream_read(const void* buf, size_t bytes, int workgroups, void* sink, void* stream) {
+  if (!buf || !sink || workgroups <= 0 || (bytes % 16)) return NSV_ERR_ARG;
+  if (bytes == 0) return NSV_OK;
+  const size_t per = ((bytes + workgroups - 1) / workgroups + 15) & ~(size_t)15;
+  hipLaunchKernelGGL(stream_read_kernel, dim3(workgroups), dim3(512), 0, (hipStream_t)stream, (const char*)buf, per,
+                     bytes, (uint32_t*)sink);
   return nsv_launch_status();
 }
 
