@@ -167,8 +167,12 @@ int nsv_store_kv(const void* key, const void* value, void* k_cache,
  *   out_tokens [B, K+1] int32: accepted drafts then the correction / bonus
  *   token; out_len [B] int32 in 1..num_drafts[b]+1
  * K <= 32.  Workspace: nsv_accept_workspace_size(B, K, V, dtype,
- * stochastic); no initialisation needed.  Argmax ties go to the lowest
- * index and NaN counts as the maximum, torch's rule.
+ * stochastic) bytes of per-chunk partial results; no initialisation
+ * needed; calls that share a workspace must not run concurrently.  Greedy
+ * acceptance is two kernels (chunk argmax, walk); stochastic acceptance
+ * five (row statistics, accept walk, residual sums (only with draft rows),
+ * samples, output tokens).  Argmax ties go to the lowest index and NaN
+ * counts as the maximum, torch's rule.
  */
 size_t nsv_accept_workspace_size(int B, int K, int V, int dtype, int stochastic);
 int nsv_accept_greedy(const void* target_logits, int64_t target_seq_stride,

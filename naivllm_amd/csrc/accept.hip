@@ -4,8 +4,18 @@
 // Behaviour follows src/myvllm/spec_engine/rejection_sampler.py:25-98 and
 // the engine's batched greedy path (spec_llm_engine.py:224-243); the
 // decomposition is this library's own.  Every pass over the vocabulary is
-// split into chunks so that a round's rows cover the chip; per-chunk results
-// go to the workspace and a small per-sequence kernel combines them.
+// split into chunks so that a round's rows cover the chip; each workgroup
+// holds its chunk in registers (16-byte loads, all issued before any is
+// used), so a row is read from HBM once per pass.  Per-chunk results go to
+// the workspace and a per-sequence kernel combines them, every entry loaded
+// in one round trip:
+//   greedy      chunk argmax keys | walk
+//   stochastic  chunk (max, sum exp) of every row | accept walk |
+//               residual sums of the resampled row (model drafts) |
+//               chunk argmax of prob / q | output tokens
+// (Combining in the last workgroup to finish, behind an arrival counter per
+// sequence, was measured slower: a few hundred same-address device-scope
+// atomics per sequence serialise at ~20 ns each, far above a launch gap.)
 //
 // Arithmetic contract (shared with the CPU oracle): torch ops on bf16/fp32
 // tensors compute in fp32 and round to the tensor dtype.  Softmax values and
@@ -17,19 +27,41 @@
 // the uniforms of the accept test are fp32.
 
 #include "common.h"
+#include "exp_f64.h"
 
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / 64;
 constexpr int kMaxK = 32;  // drafts per sequence the kernels handle
+// row-statistics / argmax pass: a chunk is read in slabs of kThreads*EPT
+// elements, EPT per thread held in registers (EPT = 32, or 8 when few rows
+// would leave the chip idle); at most kMaxChunks chunks per row (longer
+// chunks take several slabs)
+constexpr int kEptWide = 32;
+constexpr int kEptNarrow = 8;
+constexpr int kMaxChunks = 128;
+// residual / sample pass (one or a few rows per sequence): smaller chunks
+constexpr int kEpt2 = 8;
+constexpr int kChunk2 = kThreads * kEpt2;
+// rows per wave whose chunk entries are loaded in one round trip when a
+// sequence's rows are combined
+constexpr int kRowsPerWave = 9;
 
 // ---------------------------------------------------------------------------
 // element access and dtype rounding
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float load_elem(const void* base, int64_t i, int dtype) {
-  if (dtype == NSV_BF16) return bf16_bits_to_f32(((const uint16_t*)base)[i]);
-  return ((const float*)base)[i];
-}
+template <typename T> struct Elem;
+template <> struct Elem<uint16_t> {  // bf16 bits
+  __device__ static float get(uint16_t v) { return bf16_bits_to_f32(v); }
+  __device__ static float unpack(const u32x4& w, int e) {
+    return bf16_bits_to_f32((e & 1) ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffffu));
+  }
+};
+template <> struct Elem<float> {
+  __device__ static float get(float v) { return v; }
+  __device__ static float unpack(const u32x4& w, int e) { return __uint_as_float(w[e]); }
+};
 
 // fp32 value rounded to the dtype (bf16: round to nearest even)
 __device__ __forceinline__ float round_dt(float f, int dtype) {
@@ -37,12 +69,78 @@ __device__ __forceinline__ float round_dt(float f, int dtype) {
   return f;
 }
 
-// exact quantity (fp64) rounded to fp32, then to the dtype
+// fp64 quantity rounded to fp32, then to the dtype
 __device__ __forceinline__ float round_dt_d(double x, int dtype) { return round_dt((float)x, dtype); }
 
 // torch's a / b on dtype tensors: IEEE fp32 division rounded to the dtype
 // (hipcc keeps fp32 division correctly rounded: -fhip-fp32-correctly-rounded-divide-sqrt is its default)
 __device__ __forceinline__ float div_dt(float a, float b, int dtype) { return round_dt(a / b, dtype); }
+
+// the fp64 exp table, copied into LDS by a workgroup's first 64 threads
+// (visible after the workgroup's next barrier)
+__device__ __forceinline__ void load_exp_table(double* tab) {
+  if (threadIdx.x < 64) tab[threadIdx.x] = kExp2Frac64[threadIdx.x];
+}
+
+// softmax value of one element: exp(z - m) * (1 / s) in fp64 (within a few
+// fp64 ulps of the exact quotient), rounded to fp32 and then to the dtype
+__device__ __forceinline__ float prob_of(float z, float m, double inv_s, int dtype, const double* tab) {
+  return round_dt_d(nsv_exp_nonpos((double)z - (double)m, tab) * inv_s, dtype);
+}
+
+// ---------------------------------------------------------------------------
+// a slab of a row in registers: x[j] holds element slab_index(lo, j) for
+// indices below hi and -inf past it.  Thread t holds groups of kGroup
+// consecutive elements, group g at lo + kGroup*(t + g*kThreads), so every
+// row of a kernel (logits of either dtype, noise) shares one element order;
+// a 16-byte aligned row is read with 16-byte loads, any other element by
+// element.
+// ---------------------------------------------------------------------------
+constexpr int kGroup = 8;
+
+__device__ __forceinline__ int64_t slab_index(int64_t lo, int j) {
+  return lo + (int64_t)kGroup * (threadIdx.x + (j / kGroup) * kThreads) + (j % kGroup);
+}
+
+template <typename T>
+__device__ __forceinline__ bool aligned16(const T* p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15) == 0;
+}
+
+template <typename T, int EPT>
+__device__ __forceinline__ void load_slab(const T* row, int64_t lo, int64_t hi, float (&x)[EPT]) {
+  constexpr int PER = 16 / sizeof(T);       // elements per 16-byte load
+  constexpr int L = kGroup / PER;           // loads per group
+  constexpr int G = EPT / kGroup;           // groups per thread
+  static_assert(EPT % kGroup == 0 && kGroup % PER == 0, "slab shape");
+  if (aligned16(row)) {  // lo is a multiple of kGroup: group starts stay aligned
+    u32x4 w[G][L];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int64_t v0 = slab_index(lo, g * kGroup);
+#pragma unroll
+      for (int l = 0; l < L; ++l)
+        w[g][l] = v0 + kGroup <= hi ? *reinterpret_cast<const u32x4*>(row + v0 + l * PER) : u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const int64_t v0 = slab_index(lo, g * kGroup);
+      const bool whole = v0 + kGroup <= hi;
+#pragma unroll
+      for (int e = 0; e < kGroup; ++e) {
+        float f = Elem<T>::unpack(w[g][e / PER], e % PER);
+        if (!whole) f = v0 + e < hi ? Elem<T>::get(row[v0 + e]) : -__builtin_inff();  // the row's ragged end
+        x[g * kGroup + e] = f;
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+      const int64_t v = slab_index(lo, j);
+      x[j] = v < hi ? Elem<T>::get(row[v]) : -__builtin_inff();
+    }
+  }
+}
 
 // ---------------------------------------------------------------------------
 // argmax as a 64-bit max: high word = the value's order-preserving bits
@@ -60,29 +158,18 @@ __device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
 }
 __device__ __forceinline__ uint32_t key_index(uint64_t k) { return ~(uint32_t)(k & 0xffffffffu); }
 
-__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const uint64_t w = __shfl_xor(v, o, NSV_WAVE);
-    v = w > v ? w : v;
-  }
-  return v;
-}
+__device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) { return wave_max_u64_dpp(v); }
+__device__ __forceinline__ double wave_sum_d(double v) { return wave_sum_dpp(v); }
+__device__ __forceinline__ float wave_max_f(float v) { return wave_max_dpp(v); }
 
-__device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, NSV_WAVE);
-  return v;
-}
-
-// workgroup reductions through a small LDS array (kThreads / 64 waves)
+// workgroup reductions through a small LDS array (one slot per wave)
 __device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t* red) {
   v = wave_max_u64(v);
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if (lane == 0) red[w] = v;
   __syncthreads();
   uint64_t r = red[0];
-  for (int i = 1; i < kThreads / 64; ++i) r = red[i] > r ? red[i] : r;
+  for (int i = 1; i < kWaves; ++i) r = red[i] > r ? red[i] : r;
   __syncthreads();
   return r;
 }
@@ -92,30 +179,118 @@ __device__ __forceinline__ double block_sum_d(double v, double* red) {
   if (lane == 0) red[w] = v;
   __syncthreads();
   double r = 0.0;
-  for (int i = 0; i < kThreads / 64; ++i) r += red[i];  // fixed order: deterministic
+  for (int i = 0; i < kWaves; ++i) r += red[i];  // fixed order: deterministic
   __syncthreads();
   return r;
 }
 __device__ __forceinline__ float block_max_f(float v, float* red) {
-  v = wave_max(v);
+  v = wave_max_f(v);
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
   if (lane == 0) red[w] = v;
   __syncthreads();
   float r = red[0];
-  for (int i = 1; i < kThreads / 64; ++i) r = fmaxf(r, red[i]);
+  for (int i = 1; i < kWaves; ++i) r = fmaxf(r, red[i]);
   __syncthreads();
   return r;
 }
 
+// chunking of the row-statistics pass: nch chunks of `per` elements (a
+// multiple of 8, so chunk starts keep 16-byte alignment)
 struct Chunk {
   int64_t lo, hi;
 };
 __device__ __forceinline__ Chunk chunk_of(int ch, int nch, int V) {
-  const int64_t per = ((int64_t)V + nch - 1) / nch;
+  const int64_t per = (((int64_t)V + nch - 1) / nch + 7) & ~(int64_t)7;
   Chunk c;
   c.lo = min((int64_t)V, ch * per);
   c.hi = min((int64_t)V, c.lo + per);
   return c;
+}
+__device__ __forceinline__ Chunk chunk2_of(int ch, int V) {
+  Chunk c;
+  c.lo = min((int64_t)V, (int64_t)ch * kChunk2);
+  c.hi = min((int64_t)V, c.lo + kChunk2);
+  return c;
+}
+
+// First index of the maximum of a thread's slab values (NaN above every
+// number and the first NaN wins, -0 == +0, torch's argmax), as the argmax
+// key of that element; 0 when every slot lies past hi.  Slot order is index
+// order, so a strict comparison keeps the first of equal values.
+template <int EPT>
+__device__ __forceinline__ uint64_t thread_argmax(const float (&x)[EPT], int64_t lo, int64_t hi) {
+  float best = x[0];
+  int bj = 0;
+  bool nan = x[0] != x[0];
+#pragma unroll
+  for (int j = 1; j < EPT; ++j) {
+    const bool gt = x[j] > best;
+    best = gt ? x[j] : best;
+    bj = gt ? j : bj;
+    nan |= x[j] != x[j];
+  }
+  if (nan) {
+#pragma unroll
+    for (int j = EPT - 1; j >= 0; --j)
+      if (x[j] != x[j]) {
+        best = x[j];
+        bj = j;
+      }
+  }
+  const int64_t v = slab_index(lo, bj);
+  return v < hi ? argmax_key(best, (uint32_t)v) : 0ull;
+}
+
+// argmax key of a thread's elements of chunk c of a row (several slabs
+// when the chunk is longer than kThreads*EPT)
+template <typename T, int EPT>
+__device__ __forceinline__ uint64_t chunk_argmax(const T* row, const Chunk& c) {
+  uint64_t best = 0;
+  for (int64_t lo = c.lo; lo < c.hi; lo += (int64_t)kThreads * EPT) {
+    float x[EPT];
+    load_slab<T, EPT>(row, lo, c.hi, x);
+    const uint64_t k = thread_argmax<EPT>(x, lo, c.hi);
+    best = k > best ? k : best;
+  }
+  return best;
+}
+
+// ---------------------------------------------------------------------------
+// Greedy walk (rejection_sampler.py:25-36) of one sequence over its
+// per-chunk argmax keys [K+1][nch] (one workgroup).  Every key and draft is
+// loaded before kb is needed, so the walk costs one round trip.
+// ---------------------------------------------------------------------------
+__device__ void greedy_walk(const uint64_t* keys, int nch, int K, int kb, const int32_t* drafts, int32_t* out,
+                            int32_t* out_len) {
+  __shared__ uint64_t sKey[kMaxK + 1];
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int32_t d = lane < K ? drafts[lane] : 0;
+  for (int r0 = 0; r0 <= K; r0 += kWaves * kRowsPerWave) {
+    uint64_t k[kRowsPerWave][2];
+#pragma unroll
+    for (int j = 0; j < kRowsPerWave; ++j) {
+      const int r = r0 + w + j * kWaves;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int c = lane + 64 * h;
+        k[j][h] = (r <= K && c < nch) ? keys[(int64_t)r * nch + c] : 0ull;
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < kRowsPerWave; ++j) {
+      const int r = r0 + w + j * kWaves;
+      const uint64_t m = wave_max_u64(k[j][0] > k[j][1] ? k[j][0] : k[j][1]);
+      if (r <= K && lane == 0) sKey[r] = m;
+    }
+  }
+  __syncthreads();
+  if (w != 0) return;
+  const int32_t amax = lane <= kb ? (int32_t)key_index(sKey[lane]) : 0;
+  const uint64_t miss = __ballot(lane < kb && d != amax);
+  const int n = miss ? __ffsll((long long)miss) - 1 : kb;  // drafts accepted
+  if (lane < n) out[lane] = d;
+  if (lane == n) out[n] = amax;  // the correction, or the bonus token
+  if (lane == 0) *out_len = n + 1;
 }
 
 // ---------------------------------------------------------------------------
@@ -126,85 +301,31 @@ struct GreedyArgs {
   int64_t seq_stride;  // rows between sequences
   const int32_t* drafts;
   const int32_t* num_drafts;
-  int B, K, V, dtype, nch;
+  int B, K, V, nch;
   uint64_t* keys;  // [B, K+1, nch]
   int32_t* out_tokens;
   int32_t* out_len;
 };
 
 // grid (B*(K+1), nch): argmax key of one chunk of one row
+template <typename T, int EPT>
 __global__ __launch_bounds__(kThreads) void greedy_argmax_kernel(GreedyArgs a) {
-  __shared__ uint64_t red[kThreads / 64];
+  __shared__ uint64_t red[kWaves];
   const int rowid = blockIdx.x, ch = blockIdx.y;
   const int b = rowid / (a.K + 1), r = rowid - b * (a.K + 1);
   const int kb = min(max(a.num_drafts[b], 0), a.K);
   if (r > kb) return;  // uniform: a row the sequence does not use
-  // chunks of a multiple of 8 elements, so that 16-byte loads stay aligned
-  // (the maximum does not depend on how the row is cut)
-  const int64_t per = (((int64_t)a.V + a.nch - 1) / a.nch + 7) & ~(int64_t)7;
-  const int64_t base = ((int64_t)b * a.seq_stride + r) * a.V;
-  uint64_t best = 0;
-  int64_t lo = min((int64_t)a.V, ch * per), hi = min((int64_t)a.V, lo + per);
-  if (a.dtype == NSV_BF16 && ((base + lo) & 7) == 0) {
-    // 8 elements per 16-byte load, two loads in flight per iteration; the
-    // rest of the chunk (fewer than 8 elements) below
-    const int64_t nvec = (hi - lo) >> 3;
-    const u32x4* src = reinterpret_cast<const u32x4*>((const uint16_t*)a.logits + base + lo);
-    for (int64_t j = threadIdx.x; j < nvec; j += 2 * kThreads) {
-      u32x4 w[2];
-#pragma unroll
-      for (int u = 0; u < 2; ++u) w[u] = j + u * kThreads < nvec ? src[j + u * kThreads] : u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        if (j + u * kThreads >= nvec) break;
-        const uint32_t v0 = (uint32_t)(lo + ((j + u * kThreads) << 3));
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const uint32_t bits = (e & 1) ? (w[u][e >> 1] >> 16) : (w[u][e >> 1] & 0xffffu);
-          const uint64_t k = argmax_key(bf16_bits_to_f32(bits), v0 + e);
-          best = k > best ? k : best;
-        }
-      }
-    }
-    lo += nvec << 3;
-  }
-  for (int64_t v = lo + threadIdx.x; v < hi; v += kThreads) {
-    const uint64_t k = argmax_key(load_elem(a.logits, base + v, a.dtype), (uint32_t)v);
-    best = k > best ? k : best;
-  }
-  best = block_max_u64(best, red);
+  const T* row = (const T*)a.logits + ((int64_t)b * a.seq_stride + r) * a.V;
+  const uint64_t best = block_max_u64(chunk_argmax<T, EPT>(row, chunk_of(ch, a.nch, a.V)), red);
   if (threadIdx.x == 0) a.keys[(int64_t)rowid * a.nch + ch] = best;
 }
 
-// grid B: argmax per row, then rejection_sampler.py:25-36
-__global__ __launch_bounds__(64) void greedy_finalize_kernel(GreedyArgs a) {
-  const int b = blockIdx.x, lane = threadIdx.x;
-  const int kb = min(max(a.num_drafts[b], 0), a.K);
-  __shared__ int32_t amax[kMaxK + 1];
-  for (int r = 0; r <= kb; ++r) {
-    uint64_t best = 0;
-    for (int ch = lane; ch < a.nch; ch += 64) {
-      const uint64_t k = a.keys[((int64_t)b * (a.K + 1) + r) * a.nch + ch];
-      best = k > best ? k : best;
-    }
-    best = wave_max_u64(best);
-    if (lane == 0) amax[r] = (int32_t)key_index(best);
-  }
-  __syncthreads();
-  if (lane != 0) return;
-  int n = 0;
-  int32_t* out = a.out_tokens + (int64_t)b * (a.K + 1);
-  for (int i = 0; i < kb; ++i) {
-    const int32_t d = a.drafts[(int64_t)b * a.K + i];
-    if (d != amax[i]) {
-      out[n++] = amax[i];
-      a.out_len[b] = n;
-      return;
-    }
-    out[n++] = d;
-  }
-  out[n++] = amax[kb];  // every draft accepted: the bonus token
-  a.out_len[b] = n;
+// grid B: the walk of each sequence
+__global__ __launch_bounds__(kThreads) void greedy_finalize_kernel(GreedyArgs a) {
+  const int b = blockIdx.x;
+  const int nd = a.num_drafts[b];
+  greedy_walk(a.keys + (int64_t)b * (a.K + 1) * a.nch, a.nch, a.K, min(max(nd, 0), a.K), a.drafts + (int64_t)b * a.K,
+              a.out_tokens + (int64_t)b * (a.K + 1), a.out_len + b);
 }
 
 // ---------------------------------------------------------------------------
@@ -218,30 +339,34 @@ struct StochArgs {
   const int32_t* drafts;     // [B, K]
   const int32_t* num_drafts; // [B]
   const float* temperature;  // [B]
-  const float* uniforms;     // [B, K]
+  const float* uniforms;     // [B, K] (nullable without draft rows)
   const void* noise;         // sequence b's noise at b * q_seq: [V] (draft rows) or [K+1, V] (none)
   const int32_t* row_mode;   // nullable [B]: 0 = sequence b has no draft rows (n-gram mode)
   int64_t q_seq;
-  int B, K, V, dtype, nch;
+  int B, K, V;
+  int rows;                  // statistics rows per sequence in the grid: 2K+1 with draft rows, else K+1
+  int nch;                   // chunks per row of the statistics pass
+  int nch2;                  // chunks per row of the residual / sample passes
   int cdtype;                // dtype results are rounded to (the logits dtype, or fp32 for the sampler)
-  int ndtype;                // dtype of the noise
   // workspace
-  float* st_max;     // [B, 2K+1, nch]  chunk max of z = x / T
-  double* st_sum;    // [B, 2K+1, nch]  chunk sum of exp(z - chunk max)
-  uint64_t* st_key;  // [B, K+1, nch]   chunk argmax of the raw target row (greedy sequences)
-  float* row_m;      // [B, 2K+1]
-  double* row_s;     // [B, 2K+1]
-  int32_t* dec;      // [B, 4]: row to sample (-1: none), kind (0 bonus / n-gram row, 1 resample),
-                     //         accepted count, greedy flag
-  int32_t* acc;      // [B, K+1] accepted prefix
-  double* res_sum;   // [B, nch, 2]  chunk sums of the residual and of p_t
-  uint64_t* smp_key; // [B, K+1, nch] chunk argmax of prob / q
-  int32_t* out_tokens;       // sequence b's tokens at b * out_seq
+  float* st_max;       // [B, 2K+1, nch]  chunk max of z = x / T
+  double* st_sum;      // [B, 2K+1, nch]  chunk sum of exp(z - chunk max)
+  uint64_t* st_key;    // [B, K+1, nch]   chunk argmax of the raw target row (greedy sequences)
+  float* zpos;         // [B, 2K+1]       z at the row's draft token (rows 0..K-1, K+1..2K)
+  float* row_m;        // [B, 2K+1]
+  double* row_s;       // [B, 2K+1]
+  int32_t* dec;        // [B, 4]: row to sample, kind (0 bonus / n-gram rows, 1 resample),
+                       //         accepted count, greedy flag (sequence already finished)
+  int32_t* acc;        // [B, K+1] accepted prefix
+  double* res_part;    // [B, nch2, 2]  chunk sums of the residual and of p_t
+  uint64_t* smp_key;   // [B, K+1, nch2] chunk argmax of prob / q
+  int32_t* out_tokens; // sequence b's tokens at b * out_seq
   int64_t out_seq;
   int32_t* out_len;
 };
 
-__device__ __forceinline__ bool is_greedy(const StochArgs& a, int b) { return a.temperature[b] <= 1e-6f; }
+__device__ __forceinline__ bool greedy_t(float T) { return T <= 1e-6f; }
+__device__ __forceinline__ bool is_greedy(const StochArgs& a, int b) { return greedy_t(a.temperature[b]); }
 // sequence b is verified against draft rows (min(1, p_t/p_d)) rather than
 // by sampling every target row (n-gram drafts)
 __device__ __forceinline__ bool has_rows(const StochArgs& a, int b) {
@@ -251,172 +376,193 @@ __device__ __forceinline__ int kdrafts(const StochArgs& a, int b) {
   return a.K == 0 ? 0 : min(max(a.num_drafts[b], 0), a.K);  // K = 0: the sampler (no drafts)
 }
 __device__ __forceinline__ int64_t trow(const StochArgs& a, int b, int r) { return ((int64_t)b * a.t_seq + r) * a.V; }
-__device__ __forceinline__ int64_t drow(const StochArgs& a, int b, int i) { return ((int64_t)b * a.d_seq + (int64_t)i * a.d_row) * a.V; }
+__device__ __forceinline__ int64_t drow(const StochArgs& a, int b, int i) {
+  return ((int64_t)b * a.d_seq + (int64_t)i * a.d_row) * a.V;
+}
 
 // z = x / T rounded to the compute dtype (rejection_sampler.py:47, :52;
-// layers/sampler.py:20 divides by an fp32 tensor, so there it is fp32)
-__device__ __forceinline__ float scaled(const StochArgs& a, const void* base, int64_t i, float T) {
-  return div_dt(load_elem(base, i, a.dtype), T, a.cdtype);
+// layers/sampler.py:20 divides by an fp32 tensor, so there it is fp32).
+// x / 1 is x, already representable in both dtypes.
+__device__ __forceinline__ float scale_by(float x, float T, bool unit, int cdtype) {
+  return unit ? x : div_dt(x, T, cdtype);
 }
 
-// softmax value round(exp(z - m) / s) of one element
-__device__ __forceinline__ float prob_of(float z, float m, double s, int dtype) {
-  return round_dt_d(exp((double)z - (double)m) / s, dtype);
-}
-
-// grid (B*(2K+1), nch).  Rows 0..K: target rows; K+1..2K: draft rows.
-// Stochastic sequences: chunk max and sum of exp(z - max).  Greedy
-// sequences: chunk argmax of the raw target row.
+// grid (B*rows, nch).  Rows 0..K: target rows; K+1..2K: draft rows.
+// Stochastic sequences: chunk max and sum of exp(z - max), and z at the
+// row's draft token when this chunk holds it.  Greedy sequences: chunk
+// argmax of the raw target row.
+template <typename T, int EPT>
 __global__ __launch_bounds__(kThreads) void stoch_stats_kernel(StochArgs a) {
-  __shared__ float redf[kThreads / 64];
-  __shared__ double redd[kThreads / 64];
-  __shared__ uint64_t redk[kThreads / 64];
+  __shared__ float redf[kWaves];
+  __shared__ double redd[kWaves];
+  __shared__ uint64_t redk[kWaves];
+  __shared__ double etab[64];
+  constexpr int SLAB = kThreads * EPT;
   const int R = 2 * a.K + 1;
   const int rowid = blockIdx.x, ch = blockIdx.y;
-  const int b = rowid / R, r = rowid - b * R;
+  const int b = rowid / a.rows, r = rowid - b * a.rows;
   const int kb = kdrafts(a, b);
   const bool greedy = is_greedy(a, b);
   const bool is_draft = r > a.K;
-  if (!is_draft && r > kb) return;
-  if (is_draft && (greedy || !has_rows(a, b) || r - a.K - 1 >= kb)) return;
+  const int i = is_draft ? r - a.K - 1 : r;  // draft index of the row
+  // the row's draft token (loaded with the metadata; the accept test needs its z)
+  const int32_t dtok = i < a.K ? a.drafts[(int64_t)b * a.K + i] : -1;
+  const bool rows = has_rows(a, b);
+  const bool active = is_draft ? (!greedy && rows && i < kb) : r <= kb;
+  if (!active) return;  // uniform
   const Chunk c = chunk_of(ch, a.nch, a.V);
-  const int64_t slot = (int64_t)rowid * a.nch + ch;
+  const int64_t slot = ((int64_t)b * R + r) * a.nch + ch;
   if (greedy) {
-    const int64_t base = trow(a, b, r);
-    uint64_t best = 0;
-    for (int64_t v = c.lo + threadIdx.x; v < c.hi; v += kThreads) {
-      const uint64_t k = argmax_key(load_elem(a.target, base + v, a.dtype), (uint32_t)v);
-      best = k > best ? k : best;
-    }
-    best = block_max_u64(best, redk);
+    const T* row = (const T*)a.target + trow(a, b, r);
+    const uint64_t best = block_max_u64(chunk_argmax<T, EPT>(row, c), redk);
     if (threadIdx.x == 0) a.st_key[((int64_t)b * (a.K + 1) + r) * a.nch + ch] = best;
     return;
   }
-  const float T = a.temperature[b];
-  const void* src = is_draft ? a.draft : a.target;
-  const int64_t base = is_draft ? drow(a, b, r - a.K - 1) : trow(a, b, r);
+  load_exp_table(etab);
+  const float Tb = a.temperature[b];
+  const bool unit = Tb == 1.0f;
+  const T* row = (const T*)(is_draft ? a.draft : a.target) + (is_draft ? drow(a, b, i) : trow(a, b, r));
+  // z at the draft token (draft rows, and target rows before the bonus row):
+  // the chunk that holds it reads it with its slab
+  const int32_t d = rows && i < kb ? dtok : -1;
+  const bool own_d = threadIdx.x == 0 && d >= c.lo && d < c.hi;
+  const float xd = own_d ? Elem<T>::get(row[d]) : 0.f;
+  // running max over the chunk's slabs (one slab when the chunk fits);
+  // each thread's sum is rescaled when the max grows
   float m = -__builtin_inff();
-  for (int64_t v = c.lo + threadIdx.x; v < c.hi; v += kThreads) m = fmaxf(m, scaled(a, src, base + v, T));
-  m = block_max_f(m, redf);
   double s = 0.0;
-  if (m != -__builtin_inff())
-    for (int64_t v = c.lo + threadIdx.x; v < c.hi; v += kThreads) s += exp((double)scaled(a, src, base + v, T) - (double)m);
+  bool nan = false;
+  for (int64_t lo = c.lo; lo < c.hi; lo += SLAB) {
+    float z[EPT];
+    load_slab<T, EPT>(row, lo, c.hi, z);
+    float ms = -__builtin_inff();
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) {
+      z[j] = scale_by(z[j], Tb, unit, a.cdtype);
+      ms = fmaxf(ms, z[j]);
+      nan |= z[j] != z[j];
+    }
+    const float mn = fmaxf(m, block_max_f(ms, redf));  // its barrier also publishes etab
+    if (mn == -__builtin_inff()) continue;
+    if (m != -__builtin_inff() && mn != m) s *= nsv_exp_nonpos((double)m - (double)mn, etab);
+    m = mn;
+    const double md = (double)m;
+#pragma unroll
+    for (int j = 0; j < EPT; ++j) s += nsv_exp_nonpos((double)z[j] - md, etab);  // past-the-end slots: -inf -> 0
+  }
+  if (nan && m != -__builtin_inff()) s = __builtin_nan("");
   s = block_sum_d(s, redd);
   if (threadIdx.x == 0) {
     a.st_max[slot] = m;
     a.st_sum[slot] = s;
+    if (own_d) a.zpos[(int64_t)b * R + r] = scale_by(xd, Tb, unit, a.cdtype);
   }
 }
 
-// combine the chunks of row (b, r): max M and sum of exp(z - M)
-__device__ __forceinline__ void combine_row(const StochArgs& a, int b, int r, float& M, double& S) {
-  const int64_t base = ((int64_t)b * (2 * a.K + 1) + r) * a.nch;
-  M = -__builtin_inff();
-  for (int ch = 0; ch < a.nch; ++ch) M = fmaxf(M, a.st_max[base + ch]);
-  S = 0.0;
-  if (M == -__builtin_inff()) return;
-  for (int ch = 0; ch < a.nch; ++ch) {
-    const float m = a.st_max[base + ch];
-    if (m != -__builtin_inff()) S += a.st_sum[base + ch] * exp((double)m - (double)M);
+// grid B: the accept walk of sequence b (rejection_sampler.py:51-61).
+// Combines the chunk statistics of every row into (max, sum), then decides
+// every draft at once and keeps the prefix before the first rejection.
+// Everything a stochastic sequence needs is loaded in one round trip,
+// before its metadata is known (rows it does not use are combined and
+// ignored).
+__global__ __launch_bounds__(kThreads) void stoch_decide_kernel(StochArgs a) {
+  __shared__ float sM[2 * kMaxK + 1];
+  __shared__ double sS[2 * kMaxK + 1];
+  __shared__ double etab[64];
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int K = a.K, R = 2 * K + 1, nch = a.nch;
+  const int nrows = a.rows;  // the rows the statistics pass may have written
+  load_exp_table(etab);
+  const float Tb = a.temperature[b];
+  const int nd = K == 0 ? 0 : a.num_drafts[b];
+  const bool rows = has_rows(a, b);
+  int32_t d = 0;
+  float u = 0.f, zt = -__builtin_inff(), zd = -__builtin_inff();
+  if (lane < K) {
+    d = a.drafts[(int64_t)b * K + lane];
+    if (a.uniforms) u = a.uniforms[(int64_t)b * K + lane];
+    zt = a.zpos[(int64_t)b * R + lane];
+    if (a.draft) zd = a.zpos[(int64_t)b * R + K + 1 + lane];
   }
-}
-
-// grid B, one wave.  Row statistics; greedy sequences finish here; the
-// draft-row mode walks the accept test (rejection_sampler.py:51-61) and
-// picks the row to sample from.
-__global__ __launch_bounds__(64) void stoch_decide_kernel(StochArgs a) {
-  const int b = blockIdx.x, lane = threadIdx.x;
-  const int kb = kdrafts(a, b);
-  const int R = 2 * a.K + 1;
+  const int kb = min(max(nd, 0), K);
   int32_t* dec = a.dec + 4 * b;
-  int32_t* acc = a.acc + (int64_t)b * (a.K + 1);
-  if (is_greedy(a, b)) {
-    // rejection_sampler.py:95 -> verify_greedy
-    __shared__ int32_t amax[kMaxK + 1];
-    for (int r = 0; r <= kb; ++r) {
-      uint64_t best = 0;
-      for (int ch = lane; ch < a.nch; ch += 64) {
-        const uint64_t k = a.st_key[((int64_t)b * (a.K + 1) + r) * a.nch + ch];
-        best = k > best ? k : best;
+  // row q of the grid's row list is storage row q (target 0..K, draft K+1..2K);
+  // the first batch of rows is loaded with the metadata above, before the
+  // greedy test (a barrier would wait for every load in flight)
+  for (int q0 = 0; q0 < nrows; q0 += kWaves * kRowsPerWave) {
+    float m[kRowsPerWave][2];
+    double s[kRowsPerWave][2];
+#pragma unroll
+    for (int j = 0; j < kRowsPerWave; ++j) {
+      const int q = q0 + w + j * kWaves;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int c = lane + 64 * h;
+        const bool ok = q < nrows && c < nch;
+        const int64_t e = ((int64_t)b * R + q) * nch + c;
+        m[j][h] = ok ? a.st_max[e] : -__builtin_inff();
+        s[j][h] = ok ? a.st_sum[e] : 0.0;
       }
-      best = wave_max_u64(best);
-      if (lane == 0) amax[r] = (int32_t)key_index(best);
     }
-    __syncthreads();
-    if (lane == 0) {
-      int n = 0;
-      bool all = true;
-      for (int i = 0; i < kb; ++i) {
-        const int32_t d = a.drafts[(int64_t)b * a.K + i];
-        if (d != amax[i]) {
-          acc[n++] = amax[i];
-          all = false;
-          break;
-        }
-        acc[n++] = d;
+    if (greedy_t(Tb)) break;  // uniform
+    __syncthreads();  // etab
+#pragma unroll
+    for (int j = 0; j < kRowsPerWave; ++j) {
+      const int q = q0 + w + j * kWaves;
+      const float M = wave_max_f(fmaxf(m[j][0], m[j][1]));
+      // chunks with no finite element hold sum 0 and are skipped
+      double t = 0.0;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+        if (m[j][h] != -__builtin_inff()) t += s[j][h] * nsv_exp_nonpos((double)m[j][h] - (double)M, etab);
+      double S = wave_sum_d(t);
+      if (M == -__builtin_inff()) S = 0.0;
+      if (q < nrows && lane == 0) {
+        sM[q] = M;
+        sS[q] = S;
+        a.row_m[(int64_t)b * R + q] = M;
+        a.row_s[(int64_t)b * R + q] = S;
       }
-      if (all) acc[n++] = amax[kb];  // the bonus token
-      dec[0] = -1;
-      dec[1] = 0;
-      dec[2] = n;
-      dec[3] = 1;
     }
-    return;
   }
-  // row statistics of the rows this sequence uses
-  for (int r = lane; r < R; r += 64) {
-    const bool is_draft = r > a.K;
-    if ((!is_draft && r > kb) || (is_draft && (!has_rows(a, b) || r - a.K - 1 >= kb))) continue;
-    float M;
-    double S;
-    combine_row(a, b, r, M, S);
-    a.row_m[(int64_t)b * R + r] = M;
-    a.row_s[(int64_t)b * R + r] = S;
+  if (greedy_t(Tb)) {  // rejection_sampler.py:95 -> verify_greedy; finished here
+    greedy_walk(a.st_key + (int64_t)b * (K + 1) * nch, nch, K, kb, a.drafts + (int64_t)b * K,
+                a.out_tokens + (int64_t)b * a.out_seq, a.out_len + b);
+    if (tid == 0) dec[3] = 1;
+    return;
   }
   __syncthreads();
-  if (lane != 0) return;
-  dec[3] = 0;
-  if (!has_rows(a, b)) {
-    // n-gram mode: every row 0..kb is sampled; decisions come after
-    dec[0] = kb;
-    dec[1] = 0;
-    dec[2] = 0;
-    return;
-  }
-  const float T = a.temperature[b];
-  const float floor = round_dt(1e-20f, a.cdtype);
-  int n = 0;
-  for (int i = 0; i < kb; ++i) {
-    const int32_t d = a.drafts[(int64_t)b * a.K + i];
-    const float pt = prob_of(scaled(a, a.target, trow(a, b, i) + d, T), a.row_m[(int64_t)b * R + i],
-                             a.row_s[(int64_t)b * R + i], a.cdtype);
-    const int rd = a.K + 1 + i;
-    float pd = prob_of(scaled(a, a.draft, drow(a, b, i) + d, T), a.row_m[(int64_t)b * R + rd],
-                       a.row_s[(int64_t)b * R + rd], a.cdtype);
-    pd = fmaxf(pd, floor);                                    // clamp_min(1e-20)
-    const float ratio = fminf(div_dt(pt, pd, a.cdtype), 1.0f);  // clamp(max=1)
-    if (a.uniforms[(int64_t)b * a.K + i] < ratio) {
-      acc[n++] = d;
-      continue;
+  if (w != 0) return;
+  if (!rows) {  // n-gram mode: every row 0..kb is sampled; decisions come after
+    if (lane == 0) {
+      dec[0] = kb;
+      dec[1] = 0;
+      dec[2] = 0;
+      dec[3] = 0;
     }
-    dec[0] = i;  // resample row
-    dec[1] = 1;
-    dec[2] = n;
     return;
   }
-  dec[0] = kb;  // every draft accepted: bonus row
-  dec[1] = 0;
-  dec[2] = n;
-}
-
-// p_t and p_d of element v of row r (draft-row mode)
-__device__ __forceinline__ void pt_pd(const StochArgs& a, int b, int r, int64_t v, float T, float& pt, float& pd) {
-  const int R = 2 * a.K + 1;
-  pt = prob_of(scaled(a, a.target, trow(a, b, r) + v, T), a.row_m[(int64_t)b * R + r],
-               a.row_s[(int64_t)b * R + r], a.cdtype);
-  const int rd = a.K + 1 + r;
-  pd = prob_of(scaled(a, a.draft, drow(a, b, r) + v, T), a.row_m[(int64_t)b * R + rd],
-               a.row_s[(int64_t)b * R + rd], a.cdtype);
+  // lane i decides draft i: u_i < min(1, p_t(d_i) / max(p_d(d_i), 1e-20))
+  const int i = lane;
+  bool reject = false;
+  if (i < kb) {
+    if (d < 0 || d >= a.V) zt = zd = -__builtin_inff();  // a token outside the vocabulary has probability 0
+    const float pt = prob_of(zt, sM[i], 1.0 / sS[i], a.cdtype, etab);
+    float pd = prob_of(zd, sM[K + 1 + i], 1.0 / sS[K + 1 + i], a.cdtype, etab);
+    pd = fmaxf(pd, round_dt(1e-20f, a.cdtype));                 // clamp_min(1e-20)
+    const float ratio = fminf(div_dt(pt, pd, a.cdtype), 1.0f);  // clamp(max=1)
+    reject = !(u < ratio);
+  }
+  const uint64_t rej = __ballot(reject);
+  const int n = rej ? __ffsll((long long)rej) - 1 : kb;  // drafts accepted
+  if (i < n) a.acc[(int64_t)b * (K + 1) + i] = d;
+  if (lane == 0) {
+    dec[0] = n;               // the resample row, or kb: the bonus row
+    dec[1] = n < kb ? 1 : 0;
+    dec[2] = n;
+    dec[3] = 0;
+  }
 }
 
 // residual = max(p_t - p_d, 0) rounded to the dtype (rejection_sampler.py:63)
@@ -424,154 +570,195 @@ __device__ __forceinline__ float residual_of(float pt, float pd, int dtype) {
   return fmaxf(round_dt(pt - pd, dtype), 0.f);
 }
 
-// grid (B, nch): chunk sums of the residual and of p_t over the resample row
+// grid (B, nch2): chunk sums of the residual and of p_t over the resample
+// row of sequences that rejected a draft
+template <typename T>
 __global__ __launch_bounds__(kThreads) void stoch_residual_kernel(StochArgs a) {
-  __shared__ double red[kThreads / 64];
+  __shared__ double red[kWaves];
+  __shared__ double etab[64];
   const int b = blockIdx.x, ch = blockIdx.y;
   const int32_t* dec = a.dec + 4 * b;
   if (dec[3] || dec[1] != 1) return;  // uniform: only sequences that rejected a draft
-  const int r = dec[0];
-  const float T = a.temperature[b];
-  const Chunk c = chunk_of(ch, a.nch, a.V);
+  load_exp_table(etab);
+  const int r = dec[0], R = 2 * a.K + 1;
+  const float Tb = a.temperature[b];
+  const bool unit = Tb == 1.0f;
+  const Chunk c = chunk2_of(ch, a.V);
+  float xt[kEpt2], xd[kEpt2];
+  load_slab<T, kEpt2>((const T*)a.target + trow(a, b, r), c.lo, c.hi, xt);
+  load_slab<T, kEpt2>((const T*)a.draft + drow(a, b, r), c.lo, c.hi, xd);
+  const float mt = a.row_m[(int64_t)b * R + r], md = a.row_m[(int64_t)b * R + a.K + 1 + r];
+  const double it = 1.0 / a.row_s[(int64_t)b * R + r], id = 1.0 / a.row_s[(int64_t)b * R + a.K + 1 + r];
+  __syncthreads();  // etab
   double sr = 0.0, sp = 0.0;
-  for (int64_t v = c.lo + threadIdx.x; v < c.hi; v += kThreads) {
-    float pt, pd;
-    pt_pd(a, b, r, v, T, pt, pd);
+#pragma unroll
+  for (int j = 0; j < kEpt2; ++j) {
+    if (slab_index(c.lo, j) >= c.hi) continue;
+    const float pt = prob_of(scale_by(xt[j], Tb, unit, a.cdtype), mt, it, a.cdtype, etab);
+    const float pd = prob_of(scale_by(xd[j], Tb, unit, a.cdtype), md, id, a.cdtype, etab);
     sr += (double)residual_of(pt, pd, a.cdtype);
     sp += (double)pt;
   }
   sr = block_sum_d(sr, red);
   sp = block_sum_d(sp, red);
   if (threadIdx.x == 0) {
-    a.res_sum[((int64_t)b * a.nch + ch) * 2 + 0] = sr;
-    a.res_sum[((int64_t)b * a.nch + ch) * 2 + 1] = sp;
+    a.res_part[((int64_t)b * a.nch2 + ch) * 2 + 0] = sr;
+    a.res_part[((int64_t)b * a.nch2 + ch) * 2 + 1] = sp;
   }
 }
 
-// grid (B*(K+1), nch): chunk argmax of prob / q over the rows to sample
+// grid (B, nch2, K+1 or 1): chunk argmax of prob / q over the rows to
+// sample (z = 0: the resample / bonus row of a sequence with draft rows;
+// z = r: row r of an n-gram sequence)
+template <typename T, typename TQ>
 __global__ __launch_bounds__(kThreads) void stoch_sample_kernel(StochArgs a) {
-  __shared__ uint64_t red[kThreads / 64];
-  __shared__ float sS;
-  __shared__ int sUseRes;
-  const int rowid = blockIdx.x, ch = blockIdx.y;
-  const int b = rowid / (a.K + 1), r = rowid - b * (a.K + 1);
+  __shared__ uint64_t red[kWaves];
+  __shared__ double redd[kWaves];
+  __shared__ double etab[64];
+  const int b = blockIdx.x, ch = blockIdx.y, j = blockIdx.z;
   const int32_t* dec = a.dec + 4 * b;
-  if (dec[3]) return;  // greedy sequence: done
+  if (dec[3]) return;  // greedy sequence: finished by the accept walk
   const bool ngram = !has_rows(a, b);
-  if (ngram ? r > dec[0] : r != dec[0]) return;
+  const int last_row = dec[0];
+  if (ngram ? j > last_row : j != 0) return;
+  load_exp_table(etab);
+  const int r = ngram ? j : last_row;
   const int R = 2 * a.K + 1;
-  const float T = a.temperature[b];
+  const float Tb = a.temperature[b];
+  const bool unit = Tb == 1.0f;
   const bool resample = !ngram && dec[1] == 1;
+  const Chunk c = chunk2_of(ch, a.V);
+  float xt[kEpt2], xq[kEpt2];
+  load_slab<T, kEpt2>((const T*)a.target + trow(a, b, r), c.lo, c.hi, xt);
+  load_slab<TQ, kEpt2>((const TQ*)a.noise + (int64_t)b * a.q_seq + (ngram ? (int64_t)r * a.V : 0), c.lo, c.hi, xq);
+  const float mt = a.row_m[(int64_t)b * R + r];
+  const double it = 1.0 / a.row_s[(int64_t)b * R + r];
+  float p[kEpt2];
   if (resample) {
-    if (threadIdx.x == 0) {
-      double sr = 0.0, sp = 0.0;
-      for (int j = 0; j < a.nch; ++j) {
-        sr += a.res_sum[((int64_t)b * a.nch + j) * 2 + 0];
-        sp += a.res_sum[((int64_t)b * a.nch + j) * 2 + 1];
-      }
-      const float Sr = round_dt_d(sr, a.cdtype);
-      sUseRes = Sr > 0.f;  // rejection_sampler.py:64-65
-      sS = Sr > 0.f ? Sr : round_dt_d(sp, a.cdtype);
+    float xd[kEpt2];
+    load_slab<T, kEpt2>((const T*)a.draft + drow(a, b, r), c.lo, c.hi, xd);
+    const float md = a.row_m[(int64_t)b * R + a.K + 1 + r];
+    const double id = 1.0 / a.row_s[(int64_t)b * R + a.K + 1 + r];
+    // the divisor (rejection_sampler.py:63-67): the residual sum, or p_t's
+    // when it is 0; every chunk of the row folds the chunk sums in one order
+    double tr = 0.0, tp = 0.0;
+    for (int k = threadIdx.x; k < a.nch2; k += kThreads) {
+      tr += a.res_part[((int64_t)b * a.nch2 + k) * 2 + 0];
+      tp += a.res_part[((int64_t)b * a.nch2 + k) * 2 + 1];
     }
-    __syncthreads();
-  }
-  const Chunk c = chunk_of(ch, a.nch, a.V);
-  const int64_t nbase = (int64_t)b * a.q_seq + (ngram ? (int64_t)r * a.V : 0);
-  uint64_t best = 0;
-  for (int64_t v = c.lo + threadIdx.x; v < c.hi; v += kThreads) {
-    float p;
-    if (resample) {
-      float pt, pd;
-      pt_pd(a, b, r, v, T, pt, pd);
-      p = div_dt(sUseRes ? residual_of(pt, pd, a.cdtype) : pt, sS, a.cdtype);  // :66-67 residual / sum
-    } else {
-      p = prob_of(scaled(a, a.target, trow(a, b, r) + v, T), a.row_m[(int64_t)b * R + r],
-                  a.row_s[(int64_t)b * R + r], a.cdtype);
+    tr = block_sum_d(tr, redd);  // its barriers also publish etab
+    tp = block_sum_d(tp, redd);
+    const float Sr = round_dt_d(tr, a.cdtype);
+    const bool use_res = Sr > 0.f;
+    const float S = use_res ? Sr : round_dt_d(tp, a.cdtype);
+#pragma unroll
+    for (int e = 0; e < kEpt2; ++e) {
+      const float pt = prob_of(scale_by(xt[e], Tb, unit, a.cdtype), mt, it, a.cdtype, etab);
+      const float pd = prob_of(scale_by(xd[e], Tb, unit, a.cdtype), md, id, a.cdtype, etab);
+      p[e] = div_dt(use_res ? residual_of(pt, pd, a.cdtype) : pt, S, a.cdtype);  // :66-67 residual / sum
     }
-    const float q = load_elem(a.noise, nbase + v, a.ndtype);
-    const uint64_t k = argmax_key(div_dt(p, q, a.cdtype), (uint32_t)v);  // multinomial = argmax(p / q)
-    best = k > best ? k : best;
+  } else {
+    __syncthreads();  // etab
+#pragma unroll
+    for (int e = 0; e < kEpt2; ++e) p[e] = prob_of(scale_by(xt[e], Tb, unit, a.cdtype), mt, it, a.cdtype, etab);
   }
-  best = block_max_u64(best, red);
-  if (threadIdx.x == 0) a.smp_key[(int64_t)rowid * a.nch + ch] = best;
+  // multinomial = argmax(p / q); slots past the row's end never win
+#pragma unroll
+  for (int e = 0; e < kEpt2; ++e)
+    p[e] = slab_index(c.lo, e) < c.hi ? div_dt(p[e], xq[e], a.cdtype) : -__builtin_inff();
+  const uint64_t best = block_max_u64(thread_argmax<kEpt2>(p, c.lo, c.hi), red);
+  if (threadIdx.x == 0) a.smp_key[((int64_t)b * (a.K + 1) + r) * a.nch2 + ch] = best;
 }
 
-// grid B, one wave: sampled tokens -> accepted list
-__global__ __launch_bounds__(64) void stoch_finalize_kernel(StochArgs a) {
-  const int b = blockIdx.x, lane = threadIdx.x;
+// grid B: the sampled tokens of each sequence -> its output.  Every
+// sequence row's keys are loaded with the metadata, in one round trip.
+__global__ __launch_bounds__(kThreads) void stoch_finalize_kernel(StochArgs a) {
+  __shared__ uint64_t sKey[kMaxK + 1];
+  const int b = blockIdx.x, tid = threadIdx.x;
+  const int K = a.K;
+  if (tid <= K) sKey[tid] = 0;
   const int32_t* dec = a.dec + 4 * b;
-  const int32_t* acc = a.acc + (int64_t)b * (a.K + 1);
-  int32_t* out = a.out_tokens + (int64_t)b * a.out_seq;
-  __shared__ int32_t smp[kMaxK + 1];
-  const int kb = kdrafts(a, b);
-  if (dec[3]) {  // greedy
-    if (lane == 0) {
-      for (int i = 0; i < dec[2]; ++i) out[i] = acc[i];
-      a.out_len[b] = dec[2];
-    }
-    return;
-  }
+  const int d0 = dec[0], d2 = dec[2], d3 = dec[3];
   const bool ngram = !has_rows(a, b);
-  for (int r = ngram ? 0 : dec[0]; r <= dec[0]; ++r) {
-    uint64_t best = 0;
-    for (int ch = lane; ch < a.nch; ch += 64) {
-      const uint64_t k = a.smp_key[((int64_t)b * (a.K + 1) + r) * a.nch + ch];
-      best = k > best ? k : best;
+  const int nd = K == 0 ? 0 : a.num_drafts[b];
+  const int32_t dr = tid < K ? a.drafts[(int64_t)b * K + tid] : 0;
+  const int32_t ac = tid <= K ? a.acc[(int64_t)b * (K + 1) + tid] : 0;
+  const int total = (K + 1) * a.nch2;
+  const uint64_t* keys = a.smp_key + (int64_t)b * (K + 1) * a.nch2;
+  for (int e0 = 0; e0 < total; e0 += 8 * kThreads) {  // 8 loads in flight per thread
+    uint64_t k[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int e = e0 + tid + u * kThreads;
+      k[u] = e < total ? keys[e] : 0ull;
     }
-    best = wave_max_u64(best);
-    if (lane == 0) smp[r] = (int32_t)key_index(best);
+    __syncthreads();  // sKey's zeros (and, first time round, every load above)
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int e = e0 + tid + u * kThreads;
+      if (e < total) atomicMax((unsigned long long*)&sKey[e / a.nch2], (unsigned long long)k[u]);
+    }
   }
   __syncthreads();
-  if (lane != 0) return;
+  if (d3 || tid >= 64) return;  // greedy sequence: finished by the accept walk
+  const int lane = tid;
+  int32_t* out = a.out_tokens + (int64_t)b * a.out_seq;
   if (!ngram) {
-    const int n = dec[2];
-    for (int i = 0; i < n; ++i) out[i] = acc[i];
-    out[n] = smp[dec[0]];
-    a.out_len[b] = n + 1;
+    if (lane < d2) out[lane] = ac;
+    if (lane == d2) out[d2] = (int32_t)key_index(sKey[d0]);
+    if (lane == 0) a.out_len[b] = d2 + 1;
     return;
   }
   // rejection_sampler.py:76-85: accept while the target sample equals the draft
-  int n = 0;
-  for (int i = 0; i < kb; ++i) {
-    const int32_t d = a.drafts[(int64_t)b * a.K + i];
-    out[n++] = smp[i];
-    if (smp[i] != d) {
-      a.out_len[b] = n;
-      return;
-    }
-  }
-  out[n++] = smp[kb];
-  a.out_len[b] = n;
+  const int kb = min(max(nd, 0), K);
+  const int32_t smp = lane <= kb ? (int32_t)key_index(sKey[lane]) : 0;
+  const uint64_t miss = __ballot(lane < kb && smp != dr);
+  const int n = miss ? __ffsll((long long)miss) - 1 : kb;
+  if (lane <= n) out[lane] = smp;
+  if (lane == 0) a.out_len[b] = n + 1;
 }
 
-int choose_nch(int rows, int V) {
-  int nch = (512 + rows - 1) / (rows > 0 ? rows : 1);
-  const int max_by_len = V / 2048 > 1 ? V / 2048 : 1;
-  if (nch > max_by_len) nch = max_by_len;
-  if (nch > 64) nch = 64;
-  if (nch < 1) nch = 1;
-  return nch;
+// Chunks per row of the statistics pass and the slab width: 8192-element
+// chunks (EPT 32) when the rows alone give the chip enough workgroups, else
+// 2048-element chunks (EPT 8); at most kMaxChunks either way.
+struct StatsPlan {
+  int nch, ept;
+};
+StatsPlan stats_plan(int rows, int V) {
+  StatsPlan p;
+  const int wide = (V + kThreads * kEptWide - 1) / (kThreads * kEptWide);
+  p.ept = (int64_t)rows * wide >= 1024 ? kEptWide : kEptNarrow;
+  const int n = (V + kThreads * p.ept - 1) / (kThreads * p.ept);
+  p.nch = n < 1 ? 1 : (n > kMaxChunks ? kMaxChunks : n);
+  return p;
 }
+// the workspace is sized for the larger chunk count of the two widths
+int max_stats_chunks(int V) {
+  const int n = (V + kThreads * kEptNarrow - 1) / (kThreads * kEptNarrow);
+  return n < 1 ? 1 : (n > kMaxChunks ? kMaxChunks : n);
+}
+int sample_chunks(int V) { return (V + kChunk2 - 1) / kChunk2; }
 
 size_t a256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct StochLayout {
-  size_t st_max, st_sum, st_key, row_m, row_s, dec, acc, res_sum, smp_key, total;
+  size_t st_max, st_sum, st_key, zpos, row_m, row_s, dec, acc, res_part, smp_key, total;
 };
 
-StochLayout stoch_layout(int B, int K, int nch) {
+StochLayout stoch_layout(int B, int K, int nch, int nch2) {
   StochLayout L;
   const size_t R = 2 * (size_t)K + 1, K1 = (size_t)K + 1;
   size_t off = 0;
-  L.st_max = off;  off += a256((size_t)B * R * nch * sizeof(float));
-  L.st_sum = off;  off += a256((size_t)B * R * nch * sizeof(double));
-  L.st_key = off;  off += a256((size_t)B * K1 * nch * sizeof(uint64_t));
-  L.row_m = off;   off += a256((size_t)B * R * sizeof(float));
-  L.row_s = off;   off += a256((size_t)B * R * sizeof(double));
-  L.dec = off;     off += a256((size_t)B * 4 * sizeof(int32_t));
-  L.acc = off;     off += a256((size_t)B * K1 * sizeof(int32_t));
-  L.res_sum = off; off += a256((size_t)B * nch * 2 * sizeof(double));
-  L.smp_key = off; off += a256((size_t)B * K1 * nch * sizeof(uint64_t));
+  L.st_max = off;   off += a256((size_t)B * R * nch * sizeof(float));
+  L.st_sum = off;   off += a256((size_t)B * R * nch * sizeof(double));
+  L.st_key = off;   off += a256((size_t)B * K1 * nch * sizeof(uint64_t));
+  L.zpos = off;     off += a256((size_t)B * R * sizeof(float));
+  L.row_m = off;    off += a256((size_t)B * R * sizeof(float));
+  L.row_s = off;    off += a256((size_t)B * R * sizeof(double));
+  L.dec = off;      off += a256((size_t)B * 4 * sizeof(int32_t));
+  L.acc = off;      off += a256((size_t)B * K1 * sizeof(int32_t));
+  L.res_part = off; off += a256((size_t)B * nch2 * 2 * sizeof(double));
+  L.smp_key = off;  off += a256((size_t)B * K1 * nch2 * sizeof(uint64_t));
   L.total = off;
   return L;
 }
@@ -580,14 +767,57 @@ bool bad_shape(int B, int K, int V, int dtype) {
   return B < 0 || K < 0 || K > kMaxK || V <= 0 || (dtype != NSV_F32 && dtype != NSV_BF16);
 }
 
+template <typename T>
+void launch_stats(const StochArgs& a, int ept, dim3 grid, hipStream_t s) {
+  if (ept == kEptWide) hipLaunchKernelGGL((stoch_stats_kernel<T, kEptWide>), grid, dim3(kThreads), 0, s, a);
+  else hipLaunchKernelGGL((stoch_stats_kernel<T, kEptNarrow>), grid, dim3(kThreads), 0, s, a);
+}
+
+// Fill the workspace views of `a` and launch the stochastic kernels.
+// sample_rows: K+1 when a sequence may sample every row (n-gram mode),
+// 1 when every sequence has draft rows.
+int launch_stoch(StochArgs& a, const StochLayout& L, char* ws, int ept, int sample_rows, int dtype, int ndtype,
+                 hipStream_t s) {
+  a.st_max = (float*)(ws + L.st_max);
+  a.st_sum = (double*)(ws + L.st_sum);
+  a.st_key = (uint64_t*)(ws + L.st_key);
+  a.zpos = (float*)(ws + L.zpos);
+  a.row_m = (float*)(ws + L.row_m);
+  a.row_s = (double*)(ws + L.row_s);
+  a.dec = (int32_t*)(ws + L.dec);
+  a.acc = (int32_t*)(ws + L.acc);
+  a.res_part = (double*)(ws + L.res_part);
+  a.smp_key = (uint64_t*)(ws + L.smp_key);
+  const int B = a.B;
+  const dim3 g1(B * a.rows, a.nch), g2(B, a.nch2), g3(B, a.nch2, sample_rows);
+  const bool bf = dtype == NSV_BF16;
+  if (bf) launch_stats<uint16_t>(a, ept, g1, s);
+  else launch_stats<float>(a, ept, g1, s);
+  int rc = nsv_launch_status();
+  if (rc) return rc;
+  hipLaunchKernelGGL(stoch_decide_kernel, dim3(B), dim3(kThreads), 0, s, a);
+  if ((rc = nsv_launch_status())) return rc;
+  if (a.draft) {
+    if (bf) hipLaunchKernelGGL(stoch_residual_kernel<uint16_t>, g2, dim3(kThreads), 0, s, a);
+    else hipLaunchKernelGGL(stoch_residual_kernel<float>, g2, dim3(kThreads), 0, s, a);
+    if ((rc = nsv_launch_status())) return rc;
+  }
+  if (bf && ndtype == NSV_BF16) hipLaunchKernelGGL((stoch_sample_kernel<uint16_t, uint16_t>), g3, dim3(kThreads), 0, s, a);
+  else if (bf) hipLaunchKernelGGL((stoch_sample_kernel<uint16_t, float>), g3, dim3(kThreads), 0, s, a);
+  else hipLaunchKernelGGL((stoch_sample_kernel<float, float>), g3, dim3(kThreads), 0, s, a);
+  if ((rc = nsv_launch_status())) return rc;
+  hipLaunchKernelGGL(stoch_finalize_kernel, dim3(B), dim3(kThreads), 0, s, a);
+  return nsv_launch_status();
+}
+
 }  // namespace
 
 extern "C" {
 
 size_t nsv_accept_workspace_size(int B, int K, int V, int dtype, int stochastic) {
   if (bad_shape(B, K, V, dtype)) return 0;
-  if (!stochastic) return a256((size_t)B * (K + 1) * choose_nch(B * (K + 1), V) * sizeof(uint64_t));
-  return stoch_layout(B, K, choose_nch(B * (2 * K + 1), V)).total;
+  if (!stochastic) return a256((size_t)B * (K + 1) * max_stats_chunks(V) * sizeof(uint64_t));
+  return stoch_layout(B, K, max_stats_chunks(V), sample_chunks(V)).total;
 }
 
 int nsv_accept_greedy(const void* target_logits, int64_t seq_stride, const int32_t* drafts,
@@ -598,6 +828,7 @@ int nsv_accept_greedy(const void* target_logits, int64_t seq_stride, const int32
   if (!target_logits || (!drafts && K > 0) || !num_drafts || !out_tokens || !out_len) return NSV_ERR_ARG;
   const size_t need = nsv_accept_workspace_size(B, K, V, dtype, 0);
   if (!workspace || workspace_bytes < need) return NSV_ERR_WORKSPACE;
+  const StatsPlan sp = stats_plan(B * (K + 1), V);
   GreedyArgs a;
   a.logits = target_logits;
   a.seq_stride = seq_stride;
@@ -606,53 +837,24 @@ int nsv_accept_greedy(const void* target_logits, int64_t seq_stride, const int32
   a.B = B;
   a.K = K;
   a.V = V;
-  a.dtype = dtype;
-  a.nch = choose_nch(B * (K + 1), V);
+  a.nch = sp.nch;
   a.keys = (uint64_t*)workspace;
   a.out_tokens = out_tokens;
   a.out_len = out_len;
   hipStream_t s = (hipStream_t)stream;
-  hipLaunchKernelGGL(greedy_argmax_kernel, dim3(B * (K + 1), a.nch), dim3(kThreads), 0, s, a);
-  int rc = nsv_launch_status();
-  if (rc) return rc;
-  hipLaunchKernelGGL(greedy_finalize_kernel, dim3(B), dim3(64), 0, s, a);
-  return nsv_launch_status();
-}
-
-}  // extern "C"
-
-namespace {
-
-// Fill the workspace views of `a` and launch the stochastic kernels.
-int launch_stoch(StochArgs& a, const StochLayout& L, char* ws, bool any_rows, hipStream_t s) {
-  a.st_max = (float*)(ws + L.st_max);
-  a.st_sum = (double*)(ws + L.st_sum);
-  a.st_key = (uint64_t*)(ws + L.st_key);
-  a.row_m = (float*)(ws + L.row_m);
-  a.row_s = (double*)(ws + L.row_s);
-  a.dec = (int32_t*)(ws + L.dec);
-  a.acc = (int32_t*)(ws + L.acc);
-  a.res_sum = (double*)(ws + L.res_sum);
-  a.smp_key = (uint64_t*)(ws + L.smp_key);
-  const int B = a.B, K = a.K, nch = a.nch;
-  hipLaunchKernelGGL(stoch_stats_kernel, dim3(B * (2 * K + 1), nch), dim3(kThreads), 0, s, a);
-  int rc = nsv_launch_status();
-  if (rc) return rc;
-  hipLaunchKernelGGL(stoch_decide_kernel, dim3(B), dim3(64), 0, s, a);
-  if ((rc = nsv_launch_status())) return rc;
-  if (any_rows) {
-    hipLaunchKernelGGL(stoch_residual_kernel, dim3(B, nch), dim3(kThreads), 0, s, a);
-    if ((rc = nsv_launch_status())) return rc;
+  const dim3 grid(B * (K + 1), a.nch);
+  if (dtype == NSV_BF16) {
+    if (sp.ept == kEptWide) hipLaunchKernelGGL((greedy_argmax_kernel<uint16_t, kEptWide>), grid, dim3(kThreads), 0, s, a);
+    else hipLaunchKernelGGL((greedy_argmax_kernel<uint16_t, kEptNarrow>), grid, dim3(kThreads), 0, s, a);
+  } else {
+    if (sp.ept == kEptWide) hipLaunchKernelGGL((greedy_argmax_kernel<float, kEptWide>), grid, dim3(kThreads), 0, s, a);
+    else hipLaunchKernelGGL((greedy_argmax_kernel<float, kEptNarrow>), grid, dim3(kThreads), 0, s, a);
   }
-  hipLaunchKernelGGL(stoch_sample_kernel, dim3(B * (K + 1), nch), dim3(kThreads), 0, s, a);
-  if ((rc = nsv_launch_status())) return rc;
-  hipLaunchKernelGGL(stoch_finalize_kernel, dim3(B), dim3(64), 0, s, a);
+  int rc = nsv_launch_status();
+  if (rc) return rc;
+  hipLaunchKernelGGL(greedy_finalize_kernel, dim3(B), dim3(kThreads), 0, s, a);
   return nsv_launch_status();
 }
-
-}  // namespace
-
-extern "C" {
 
 int nsv_accept_stochastic(const void* target_logits, int64_t target_seq_stride, const void* draft_logits,
                           int64_t draft_seq_stride, int64_t draft_row_stride, const int32_t* draft_mode,
@@ -671,8 +873,7 @@ int nsv_accept_stochastic(const void* target_logits, int64_t target_seq_stride, 
   const int64_t q_default = (draft_logits && !draft_mode) ? (int64_t)V : (int64_t)(K + 1) * V;
   if (noise_seq_stride == 0) noise_seq_stride = q_default;
   if (noise_seq_stride < q_default) return NSV_ERR_ARG;
-  const int nch = choose_nch(B * (2 * K + 1), V);
-  const StochLayout L = stoch_layout(B, K, nch);
+  const StochLayout L = stoch_layout(B, K, max_stats_chunks(V), sample_chunks(V));
   if (!workspace || workspace_bytes < L.total) return NSV_ERR_WORKSPACE;
   StochArgs a;
   a.target = target_logits;
@@ -690,19 +891,21 @@ int nsv_accept_stochastic(const void* target_logits, int64_t target_seq_stride, 
   a.B = B;
   a.K = K;
   a.V = V;
-  a.dtype = dtype;
+  a.rows = draft_logits ? 2 * K + 1 : K + 1;
+  const StatsPlan sp = stats_plan(B * a.rows, V);
+  a.nch = sp.nch;
+  a.nch2 = sample_chunks(V);
   a.cdtype = dtype;
-  a.ndtype = dtype;
-  a.nch = nch;
   a.out_tokens = out_tokens;
   a.out_seq = K + 1;
   a.out_len = out_len;
-  return launch_stoch(a, L, (char*)workspace, draft_logits != nullptr, (hipStream_t)stream);
+  const int sample_rows = (draft_logits && !draft_mode) ? 1 : K + 1;
+  return launch_stoch(a, L, (char*)workspace, sp.ept, sample_rows, dtype, dtype, (hipStream_t)stream);
 }
 
 size_t nsv_sample_workspace_size(int B, int V, int dtype) {
   if (bad_shape(B, 0, V, dtype)) return 0;
-  return stoch_layout(B, 0, choose_nch(B, V)).total + a256((size_t)B * sizeof(int32_t));
+  return stoch_layout(B, 0, max_stats_chunks(V), sample_chunks(V)).total + a256((size_t)B * sizeof(int32_t));
 }
 
 int nsv_sample(const void* logits, int64_t row_stride, const float* temperature, const float* noise, int B, int V,
@@ -711,8 +914,7 @@ int nsv_sample(const void* logits, int64_t row_stride, const float* temperature,
   if (bad_shape(B, 0, V, dtype) || row_stride < V || row_stride % V || out_stride < 1) return NSV_ERR_ARG;
   if (B == 0) return NSV_OK;
   if (!logits || !temperature || !noise || !out_tokens) return NSV_ERR_ARG;
-  const int nch = choose_nch(B, V);
-  const StochLayout L = stoch_layout(B, 0, nch);
+  const StochLayout L = stoch_layout(B, 0, max_stats_chunks(V), sample_chunks(V));
   if (!workspace || workspace_bytes < nsv_sample_workspace_size(B, V, dtype)) return NSV_ERR_WORKSPACE;
   StochArgs a;
   a.target = logits;
@@ -730,14 +932,15 @@ int nsv_sample(const void* logits, int64_t row_stride, const float* temperature,
   a.B = B;
   a.K = 0;
   a.V = V;
-  a.dtype = dtype;
+  a.rows = 1;
+  const StatsPlan sp = stats_plan(B, V);
+  a.nch = sp.nch;
+  a.nch2 = sample_chunks(V);
   a.cdtype = NSV_F32;  // logits / (fp32 tensor) promotes to fp32 (layers/sampler.py:20-23)
-  a.ndtype = NSV_F32;
-  a.nch = nch;
   a.out_tokens = out_tokens;
   a.out_seq = out_stride;
   a.out_len = (int32_t*)((char*)workspace + L.total);
-  return launch_stoch(a, L, (char*)workspace, false, (hipStream_t)stream);
+  return launch_stoch(a, L, (char*)workspace, sp.ept, 1, dtype, NSV_F32, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -40,6 +40,74 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// ---------------------------------------------------------------------------
+// Wave reductions on the VALU: four DPP steps combine each 16-lane row
+// (lane ^ 1, lane ^ 2, then the 8- and 16-lane mirrors, each pairing lanes
+// that hold different partial results), then the four row results are read
+// out with v_readlane and combined in the order row 0, 1, 2, 3.  No step goes
+// through the LDS pipe, whose ds_bpermute round trip (~100+ cycles) would
+// otherwise chain six times per reduction.  The result is uniform and the
+// combination order is fixed, so floating-point sums are deterministic.
+// ---------------------------------------------------------------------------
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7 - i within 8 lanes
+constexpr int kDppMirror = 0x140;     // lane i <-> 15 - i within 16 lanes
+
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __uint_as_float(dpp_u32<CTRL>(__float_as_uint(v)));
+}
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp_u64(uint64_t v) {
+  return (uint64_t)dpp_u32<CTRL>((uint32_t)v) | ((uint64_t)dpp_u32<CTRL>((uint32_t)(v >> 32)) << 32);
+}
+__device__ __forceinline__ uint32_t lane_u32(uint32_t v, int lane) {
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, lane);
+}
+__device__ __forceinline__ uint64_t lane_u64(uint64_t v, int lane) {
+  return (uint64_t)lane_u32((uint32_t)v, lane) | ((uint64_t)lane_u32((uint32_t)(v >> 32), lane) << 32);
+}
+
+__device__ __forceinline__ float wave_max_dpp(float v) {
+  v = fmaxf(v, dpp_f32<kDppXor1>(v));
+  v = fmaxf(v, dpp_f32<kDppXor2>(v));
+  v = fmaxf(v, dpp_f32<kDppHalfMirror>(v));
+  v = fmaxf(v, dpp_f32<kDppMirror>(v));
+  const float r0 = __uint_as_float(lane_u32(__float_as_uint(v), 0)), r1 = __uint_as_float(lane_u32(__float_as_uint(v), 16));
+  const float r2 = __uint_as_float(lane_u32(__float_as_uint(v), 32)), r3 = __uint_as_float(lane_u32(__float_as_uint(v), 48));
+  return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
+}
+
+__device__ __forceinline__ double wave_sum_dpp(double v) {
+  auto step = [](double x, double y) { return x + y; };
+  uint64_t u = (uint64_t)__double_as_longlong(v);
+  v = step(v, __longlong_as_double((long long)dpp_u64<kDppXor1>(u)));
+  u = (uint64_t)__double_as_longlong(v);
+  v = step(v, __longlong_as_double((long long)dpp_u64<kDppXor2>(u)));
+  u = (uint64_t)__double_as_longlong(v);
+  v = step(v, __longlong_as_double((long long)dpp_u64<kDppHalfMirror>(u)));
+  u = (uint64_t)__double_as_longlong(v);
+  v = step(v, __longlong_as_double((long long)dpp_u64<kDppMirror>(u)));
+  u = (uint64_t)__double_as_longlong(v);
+  const double r0 = __longlong_as_double((long long)lane_u64(u, 0)), r1 = __longlong_as_double((long long)lane_u64(u, 16));
+  const double r2 = __longlong_as_double((long long)lane_u64(u, 32)), r3 = __longlong_as_double((long long)lane_u64(u, 48));
+  return ((r0 + r1) + r2) + r3;
+}
+
+__device__ __forceinline__ uint64_t wave_max_u64_dpp(uint64_t v) {
+  auto mx = [](uint64_t x, uint64_t y) { return x > y ? x : y; };
+  v = mx(v, dpp_u64<kDppXor1>(v));
+  v = mx(v, dpp_u64<kDppXor2>(v));
+  v = mx(v, dpp_u64<kDppHalfMirror>(v));
+  v = mx(v, dpp_u64<kDppMirror>(v));
+  return mx(mx(lane_u64(v, 0), lane_u64(v, 16)), mx(lane_u64(v, 32), lane_u64(v, 48)));
+}
+
 // Per-head q/k RMSNorm and NeoX rotation of one rotation pair (x1, x2) =
 // (row[l], row[l + D/2]), with floating-point contraction off: every caller
 // evaluates the same IEEE operations (no fused multiply-add chosen per call
