@@ -367,9 +367,11 @@ int nsv_embed_rms_norm(const int64_t* ids, const void* embed, int64_t vocab,
  *     of the new resid^2 over each 16-column tile; y is unused.
  * N % 16 == 0, K % 8 == 0.  For 32-80 rows and fewer than 128 column tiles
  * the reduction is split over up to 4 workgroups per tile, whose partials
- * meet in `workspace` (nsv_linear_workspace_size bytes, zero-filled before
- * the first call; every call leaves its counters at zero again, so one
- * workspace serves every call on a stream); otherwise no workspace is used.
+ * meet in `workspace` (nsv_linear_workspace_size bytes: a fixed 64 KiB area
+ * of per-tile arrival counters, then fp32 partials).  The counter area must
+ * be zero before a workspace's first call; every call leaves it zero, so
+ * one workspace serves every call of any shape on a stream (calls sharing
+ * it must not run concurrently).  Otherwise no workspace is used.
  */
 size_t nsv_linear_workspace_size(int M, int N, int K);
 /* Rows of ss_out a residual-epilogue call with these M, N, K (and an

@@ -37,6 +37,13 @@ constexpr int kLinWaves = 8;
 constexpr int kLinThreads = kLinWaves * 64;
 constexpr int kBN = 16;            // output columns per workgroup
 constexpr int kMaxRows = 80;       // activation rows (5 MFMA row tiles)
+// Arrival counters of split tiles: one fixed 64 KiB area at the front of
+// the workspace, so calls of every shape find their counters at the same
+// place, zero.  Tiles 0..255 each get their own 256-byte line (device-scope
+// atomics on one line serialise, ~20 ns apiece); tile t + 256 k shares
+// t's line.  Splitting needs fewer than 128 column tiles, well inside.
+constexpr int kMaxCounterTiles = 16384;
+__device__ __forceinline__ int lin_counter_slot(int tile) { return ((tile & 255) << 6) | (tile >> 8); }
 
 struct LinearArgs {
   const uint16_t* x;       // [M, K]: activations, or the residual stream r (RMSNorm prologue)
@@ -51,7 +58,7 @@ struct LinearArgs {
   int M, N, K;
   int ks;                  // workgroups per 16-column tile, each taking a share of the reduction
   float* part;             // [N/16, ks, 80, 16] their partial products (ks > 1)
-  unsigned* counters;      // [N/16] tile workgroups done so far; every call leaves them zero
+  unsigned* counters;      // tile t's workgroups done so far at lin_counter_slot(t); every call leaves them zero
 };
 
 __device__ __forceinline__ bf16x8 to_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
@@ -292,11 +299,11 @@ __global__ __launch_bounds__(kLinThreads, lin_waves_per_eu(MT, SMALL, BNV)) void
     __syncthreads();
     __shared__ int last;
     if (tid == 0)
-      last = __hip_atomic_fetch_add(&a.counters[tile], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+      last = __hip_atomic_fetch_add(&a.counters[lin_counter_slot(tile)], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
              (unsigned)(a.ks - 1);
     __syncthreads();
     if (!last) return;
-    if (tid == 0) __hip_atomic_store(&a.counters[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) __hip_atomic_store(&a.counters[lin_counter_slot(tile)], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // the tile's total into wave 0's slot of red, zeros in the others, so the
     // epilogue below reads it unchanged
     if (tid < MP * 4 && m < M) {
@@ -453,10 +460,12 @@ LinPlan linear_plan(int M, int N, int K, bool norm, int epi, int cus) {
   return {16, ks, (int64_t)(N / kBN) * gy * ks > cus};
 }
 
+size_t linear_counter_bytes() { return (size_t)kMaxCounterTiles * sizeof(unsigned); }
+
 size_t linear_ws_bytes(int ks, int N) {
   if (ks <= 1) return 0;
   const size_t tiles = (size_t)(N / kBN);
-  return ((tiles * sizeof(unsigned) + 255) & ~(size_t)255) + tiles * ks * kMaxRows * kBN * sizeof(float);
+  return linear_counter_bytes() + tiles * ks * kMaxRows * kBN * sizeof(float);
 }
 
 template <int MT, int BNV, bool SMALL>
@@ -537,7 +546,7 @@ int nsv_linear(const void* x, const void* norm_w, const float* ss_in, int nss_in
   const LinPlan p = linear_plan(M, N, K, norm, epilogue, lin_device_cus());
   const size_t need = linear_ws_bytes(p.ks, N);
   if (need && (!workspace || workspace_bytes < need)) return NSV_ERR_WORKSPACE;
-  const size_t cnt = ((size_t)(N / kBN) * sizeof(unsigned) + 255) & ~(size_t)255;
+  const size_t cnt = linear_counter_bytes();
   LinearArgs a{(const uint16_t*)x, (const uint16_t*)norm_w, ss_in, nss_in, eps, (const uint16_t*)weight,
                (uint16_t*)y, (uint16_t*)resid, ss_out, M, N, K, p.ks,
                need ? (float*)((char*)workspace + cnt) : nullptr, need ? (unsigned*)workspace : nullptr};

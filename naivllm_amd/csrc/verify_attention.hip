@@ -43,6 +43,10 @@ constexpr int kMaxSplitPages = 1024;  // block-table entries of one split staged
 // workspace.  The area has one fixed size, so every call finds its counters
 // at the same place, zero, whatever the previous call's shape was.
 constexpr int kMaxCounterPairs = 16384;
+// Counter slot of a pair: pairs 0..255 each get their own 256-byte line
+// (device-scope atomics on one line serialise, ~20 ns apiece), and pair
+// p + 256 k shares p's line.
+__device__ __forceinline__ int counter_slot(int pair) { return ((pair & 255) << 6) | (pair >> 8); }
 #ifndef NSV_MAX_STAGES
 #define NSV_MAX_STAGES 4  // deepest key-split pipeline
 #endif
@@ -1109,11 +1113,11 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
   __syncthreads();
   __shared__ int is_last;
   if (tid == 0)
-    is_last = __hip_atomic_fetch_add(&a.counters[pair], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+    is_last = __hip_atomic_fetch_add(&a.counters[counter_slot(pair)], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
               (unsigned)(nsplit - 1);
   __syncthreads();
   if (!is_last) return;
-  if (tid == 0) __hip_atomic_store(&a.counters[pair], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) __hip_atomic_store(&a.counters[counter_slot(pair)], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   // The other splits' partials and (max, sum) pairs for this thread's items,
   // loaded CH splits per round trip (all loads of a round trip issued before
   // any is used); this split's own sums are still in registers.
