@@ -60,8 +60,10 @@ const char* nsv_error_string(int code);
  *   max_q_len     >= every cu_seqlens_q[b+1]-cu_seqlens_q[b] (host-known,
  *                 as the reference computes block_m from seqlens_q)
  *   kv_split_tokens  keys per workgroup split (multiple of 128); 0 = auto
- * Supported: D in {64, 128}; H % Hkv == 0; (H/Hkv)*max_q_len <= 64;
- * block_size a power of two.
+ * Supported: D in {64, 128}; H % Hkv == 0; max_q_len <= 64; block_size a
+ * power of two.  A kv head's rows ((H/Hkv) * max_q_len) beyond 64 are
+ * served in launches over subsets of its query heads (the largest divisor
+ * of H/Hkv whose rows fit), each re-reading the pair's K/V.
  * Workspace: nsv_verify_attention_workspace_size() bytes (0 when every
  * sequence fits one split): a 64 KiB area of per-(sequence, kv head)
  * arrival counters, then fp32 split partials.  The counter area must be

@@ -47,7 +47,7 @@ def test_verify_attention_rejects_bad_shapes_before_launch():
     assert call(D=96) == -2          # head_dim outside {64, 128}
     assert call(H=12, Hkv=8) == -2   # heads not a multiple of kv heads
     assert call(bs=100) == -2        # page size not a power of two
-    assert call(H=64, Hkv=8) == -2   # GQA group x query rows > 64
+    assert call(mq=65) == -2         # more than 64 query rows per sequence
     assert call(dt=7) == -1
     assert call(split=100) == -1     # split not a multiple of 128
     assert call(B=-1) == -1
@@ -68,15 +68,20 @@ def test_workspace_size_matches_split_plan():
     # pairs x 4 key splits fill the 256 CUs a host without a GPU assumes
     rows = 8 * 8 * 4 * 18
     assert h.nsv_verify_attention_workspace_size(8, 16, 8, 128, 256, 6, 9, 1, 0) == cnt + pad(rows * 8) + rows * 512
-    # 4 sequences: 32 pairs x 4 key splits leave half the CUs idle, so the d-sliced kernel
-    # (4 head-dim slices, 2 key splits merged by a second kernel) keeps the shape
+    # 4 sequences: 32 pairs take the key-split kernel too, 8 splits each by the CU count but
+    # none shorter than 256 keys: 6 for the 1536-key tables
     import ctypes
     kind, splits = ctypes.c_int(), ctypes.c_int()
     assert h.nsv_verify_attention_plan(4, 16, 8, 128, 256, 6, 9, 1, 0, 256, ctypes.addressof(kind),
                                        ctypes.addressof(splits)) == 0
-    assert (kind.value, splits.value) == (0, 2)
-    rows = 4 * 8 * 2 * 18
+    assert (kind.value, splits.value) == (1, 6)
+    rows = 4 * 8 * 6 * 18
     assert h.nsv_verify_attention_workspace_size(4, 16, 8, 128, 256, 6, 9, 1, 0) == cnt + pad(rows * 8) + rows * 512
+    # 2 sequences: 16 pairs keep the d-sliced kernel (4 head-dim slices, key splits merged by a
+    # second kernel)
+    assert h.nsv_verify_attention_plan(2, 16, 8, 128, 256, 6, 9, 1, 0, 256, ctypes.addressof(kind),
+                                       ctypes.addressof(splits)) == 0
+    assert kind.value == 0
     # 16-page tables (4096 keys): the key-split kernel, 4 splits per sequence for 64 pairs on
     # the 256 CUs a host without a GPU assumes
     rows = 8 * 8 * 4 * 18
@@ -89,6 +94,21 @@ def test_workspace_size_matches_split_plan():
     assert h.nsv_verify_attention_workspace_size(32, 16, 8, 128, 256, 6, 9, 1, 0) == 0
     # one split: no workspace
     assert h.nsv_verify_attention_workspace_size(1, 16, 8, 128, 256, 1, 9, 1, 256) == 0
+
+
+def test_plan_serves_large_groups_in_head_subsets():
+    # (H / Hkv) * max_q_len > 64: the plan takes the largest divisor of the group whose
+    # rows fit, and sizes the workspace for one subset's rows (the launches share it)
+    import ctypes
+    h = _lib.lib()
+    kind, splits = ctypes.c_int(), ctypes.c_int()
+    for H, mq in [(32, 17), (64, 9), (64, 33), (8, 64)]:
+        assert h.nsv_verify_attention_plan(2, H, 8, 128, 256, 24, mq, 1, 0, 256, ctypes.addressof(kind),
+                                           ctypes.addressof(splits)) == 0, (H, mq)
+    # GQA-4 x 17 rows: 2 heads (34 rows) per launch; 24-page tables -> key-split, 16 splits for 16 pairs
+    rows = 2 * 8 * 16 * 34
+    pad = lambda x: (x + 255) // 256 * 256
+    assert h.nsv_verify_attention_workspace_size(2, 32, 8, 128, 256, 24, 17, 1, 0) == 65536 + pad(rows * 8) + rows * 512
 
 
 def test_store_kv_rejects_bad_arguments():

@@ -65,6 +65,21 @@ def test_gqa4_8b_shape(dtype, max_blocks):
     assert_close(out, _oracle(vb), dtype, "gqa4")
 
 
+@pytest.mark.parametrize("dtype,max_blocks,H,ql", [("bf16", None, 32, 17), ("bf16", 24, 32, 17), ("f32", None, 32, 17),
+                                                   ("bf16", None, 64, 9), ("bf16", 24, 64, 9), ("f32", None, 64, 9)])
+def test_groups_beyond_64_rows(dtype, max_blocks, H, ql):
+    # (H / Hkv) * max_q_len > 64 rows: GQA-4 with K = 16 drafts (68 rows)
+    # and GQA-8 with K = 8 (72 rows) run as launches over subsets of each
+    # kv head's query heads (2 of 4, 4 of 8), through the d-sliced kernel
+    # (6-page tables), the key-split kernel (24 pages) and the fp32 kernel;
+    # the second sequence is ragged and carries padding rows
+    print(f"case: {H}Q/8KV {ql} rows per sequence, dtype={dtype} max_blocks={max_blocks}", flush=True)
+    vb = synth.verify_batch(23, [1100, 1500], [ql, ql - 3], num_heads=H, num_kv_heads=8, dtype=dtype,
+                            max_blocks=max_blocks, pad_rows=[0, 2])
+    out = _gpu(vb, max_q_len=ql)
+    assert_close(out, _oracle(vb), dtype, f"{H // 8} heads x {ql} rows")
+
+
 @pytest.mark.parametrize("max_blocks", [None, 16])
 def test_small_batch_many_key_splits(max_blocks):
     # few (sequence, kv head) pairs: each context is cut into many short
