@@ -277,8 +277,13 @@ __global__ __launch_bounds__(kLinThreads, lin_waves_per_eu(MT, SMALL, BNV)) void
   if (WR == kBN && a.ks > 1) {  // split reductions run on 16-column tiles only
     // ---- split-K: publish this workgroup's tile partial; the tile's last
     // workgroup to finish sums the ks partials in order (deterministic) and
-    // runs the epilogue.  Partials and the arrival counter are agent-scope
-    // (coherent across XCDs without cache maintenance).
+    // runs the epilogue.  Ordering without release/acquire (which on gfx950
+    // would write back and invalidate whole L2s): every partial is written
+    // and read with agent-scope relaxed atomics (sc1: performed at the
+    // device's point of coherence, never served from a stale cached copy);
+    // each thread waits for its stores' acknowledgement (vmcnt(0)) before the
+    // barrier that precedes the arrival atomic, and the last workgroup issues
+    // its loads only after the counter's value came back.
     const int m = tid >> 2, q = tid & 3;
     float* pt = a.part + (int64_t)tile * a.ks * (kMaxRows * kBN);
     if (tid < MP * 4 && m < M) {

@@ -1105,11 +1105,14 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
   if (nsplit == 1) return;
 
   // ---- cross-split merge by the pair's last split to finish ------------------
-  // The partials above and the (max, sum) pairs below are agent-scope stores
-  // (written through to the point of coherence of every XCD).  Once all of
-  // them are acknowledged the split counts itself in; the split that counts
-  // last reads every partial back with agent-scope loads, so no cache
-  // write-back or invalidation of a whole L2 is needed.
+  // Ordering without release/acquire (which on gfx950 would write back and
+  // invalidate whole L2s: 45 us per call measured): the partials above and
+  // the (max, sum) pairs are agent-scope relaxed atomic stores (sc1: written
+  // through to the device's point of coherence).  Every thread waits for
+  // their acknowledgement (vmcnt(0)) before the barrier that precedes the
+  // arrival atomic; the split that counts last issues its agent-scope loads
+  // (served from the point of coherence, past any cached copy) only after
+  // the counter's value came back, so it reads every other split's partials.
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   __shared__ int is_last;
