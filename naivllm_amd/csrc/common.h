@@ -28,17 +28,6 @@ __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
   return (uint16_t)(u >> 16);
 }
 
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, NSV_WAVE));
-  return v;
-}
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, NSV_WAVE);
-  return v;
-}
 
 // ---------------------------------------------------------------------------
 // Wave reductions on the VALU: four DPP steps combine each 16-lane row
@@ -98,6 +87,20 @@ __device__ __forceinline__ double wave_sum_dpp(double v) {
   const double r2 = __longlong_as_double((long long)lane_u64(u, 32)), r3 = __longlong_as_double((long long)lane_u64(u, 48));
   return ((r0 + r1) + r2) + r3;
 }
+
+__device__ __forceinline__ float wave_sum_f32_dpp(float v) {
+  v += dpp_f32<kDppXor1>(v);
+  v += dpp_f32<kDppXor2>(v);
+  v += dpp_f32<kDppHalfMirror>(v);
+  v += dpp_f32<kDppMirror>(v);
+  const float r0 = __uint_as_float(lane_u32(__float_as_uint(v), 0)), r1 = __uint_as_float(lane_u32(__float_as_uint(v), 16));
+  const float r2 = __uint_as_float(lane_u32(__float_as_uint(v), 32)), r3 = __uint_as_float(lane_u32(__float_as_uint(v), 48));
+  return ((r0 + r1) + r2) + r3;
+}
+
+// Maximum and sum over the 64 lanes of a wave (every lane active), uniform.
+__device__ __forceinline__ float wave_max(float v) { return wave_max_dpp(v); }
+__device__ __forceinline__ float wave_sum(float v) { return wave_sum_f32_dpp(v); }
 
 __device__ __forceinline__ uint64_t wave_max_u64_dpp(uint64_t v) {
   auto mx = [](uint64_t x, uint64_t y) { return x > y ? x : y; };

@@ -47,6 +47,9 @@ constexpr int kMaxCounterPairs = 16384;
 // (device-scope atomics on one line serialise, ~20 ns apiece), and pair
 // p + 256 k shares p's line.
 __device__ __forceinline__ int counter_slot(int pair) { return ((pair & 255) << 6) | (pair >> 8); }
+#ifndef NSV_KS_SHORT_TILES
+#define NSV_KS_SHORT_TILES 4  // key-split splits of at most this many tiles per wave keep one tile in flight
+#endif
 #ifndef NSV_MAX_STAGES
 #define NSV_MAX_STAGES 4  // deepest key-split pipeline
 #endif
@@ -1547,7 +1550,7 @@ int make_plan(int B, int H, int Hkv, int D, int block_size, int max_blocks, int 
     if (p->S > 8192) return NSV_ERR_UNSUPPORTED;  // the merge stages 2 * S floats in LDS
     // keys one split covers at most, and the 16-key tiles each of the 8 waves takes
     const int64_t split_keys = p->split > 0 ? p->split : (max_ctx + p->S - 1) / p->S;
-    p->ks_short = (split_keys + 16 * kKsWaves - 1) / (16 * kKsWaves) <= 4;
+    p->ks_short = (split_keys + 16 * kKsWaves - 1) / (16 * kKsWaves) <= NSV_KS_SHORT_TILES;
     return NSV_OK;
   }
   if (dtype == NSV_BF16) {
