@@ -168,7 +168,7 @@ int nsv_store_kv(const void* key, const void* value, void* k_cache,
  *   drafts [B, K] int32, num_drafts [B] int32 (clamped to 0..K)
  *   out_tokens [B, K+1] int32: accepted drafts then the correction / bonus
  *   token; out_len [B] int32 in 1..num_drafts[b]+1
- * K <= 32.  Workspace: nsv_accept_workspace_size(B, K, V, dtype,
+ * K <= 63.  Workspace: nsv_accept_workspace_size(B, K, V, dtype,
  * stochastic) bytes of per-chunk partial results; no initialisation
  * needed; calls that share a workspace must not run concurrently.  Greedy
  * acceptance is two kernels (chunk argmax, walk); stochastic acceptance

@@ -33,7 +33,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
-constexpr int kMaxK = 32;  // drafts per sequence the kernels handle
+constexpr int kMaxK = 63;  // drafts per sequence: K+1 rows fit one 64-lane ballot
 // row-statistics / argmax pass: a chunk is read in slabs of kThreads*EPT
 // elements, EPT per thread held in registers (EPT = 32, or 8 when few rows
 // would leave the chip idle); at most kMaxChunks chunks per row (longer

@@ -128,8 +128,9 @@ def test_wrappers_raise_value_error_on_rejected_arguments():
 
 def test_accept_and_ngram_reject_bad_arguments_before_launch():
     h = _lib.lib()
-    # K above 32, bad dtype, stride below K + 1, missing workspace
-    assert h.nsv_accept_greedy(1, 9, 1, 1, 2, 33, 100, 1, 1, 1, 1, 1 << 20, None) == -1
+    # K above 63 (K + 1 rows must fit one 64-lane wave), bad dtype, stride below K + 1, missing workspace
+    assert h.nsv_accept_greedy(1, 65, 1, 1, 2, 64, 100, 1, 1, 1, 1, 1 << 20, None) == -1
+    assert h.nsv_accept_workspace_size(2, 64, 100, 1, 1) == 0 and h.nsv_accept_workspace_size(2, 63, 100, 1, 1) > 0
     assert h.nsv_accept_greedy(1, 9, 1, 1, 2, 8, 100, 5, 1, 1, 1, 1 << 20, None) == -1
     assert h.nsv_accept_greedy(1, 8, 1, 1, 2, 8, 100, 1, 1, 1, 1, 1 << 20, None) == -1
     assert h.nsv_accept_greedy(1, 9, 1, 1, 2, 8, 100, 1, 1, 1, None, 0, None) == -3

@@ -229,3 +229,182 @@ def test_stochastic_mixed_draft_modes(dtype):
         else:
             want = oa.verify(drafts, rows, None, float(temps[b]), None, Q[b, :k + 1], dtype)
         assert got[b] == want, (b, got[b], want)
+
+
+# Rows cut into chunks longer than one slab: the statistics pass rescales its
+# running sum when a later slab raises the chunk maximum, and the argmax
+# passes compare keys across slabs.  V = 300000 with few rows takes the
+# narrow slabs (128 chunks of 2344 elements: slabs of 2048 + 296); V = 1.1M
+# with 9 rows takes the wide ones (128 chunks of 8600: slabs of 8192 + 408).
+def slab_of(V):
+    """The slab length these tests' row counts select: narrow below 1M, wide above."""
+    return 2048 if V < 10 ** 6 else 8192
+
+
+def plant_second_slabs(x, V, seed):
+    """Large values in the second slab of some chunks (the maximum of those
+    chunks arrives after the first slab) and an exact tie between the two
+    slabs of another chunk."""
+    per = ((V + 127) // 128 + 7) & ~7
+    slab = slab_of(V)
+    rng = np.random.default_rng(seed)
+    for r in range(x.shape[0]):
+        for c in rng.choice(127, 6, replace=False):  # the last chunk is short: it may hold one slab only
+            x[r, c * per + slab + int(rng.integers(0, per - slab))] = 8.0 + rng.random()
+        c = int(rng.integers(0, 127))
+        x[r, c * per + 3] = x[r, c * per + slab + 5] = 12.0  # equal row maxima in both slabs: the first index wins
+    return x
+
+
+@pytest.mark.parametrize("dtype,V", [("bf16", 300000), ("f32", 300000), ("bf16", 1100000)])
+def test_greedy_multi_slab_chunks(dtype, V):
+    print(f"case: greedy multi-slab {dtype} V={V}", flush=True)
+    K = 2 if V < 10 ** 6 else 8
+    B = 2 if V < 10 ** 6 else 1
+    x = plant_second_slabs(synth.normal(70, 71, B * (K + 1) * V, 2.0).reshape(B * (K + 1), V), V, 72)
+    per = ((V + 127) // 128 + 7) & ~7
+    x[1, 40 * per + slab_of(V) + 1] = np.nan  # in a second slab; NaN beats every number
+    lg = torch.from_numpy(x.astype(np.float32)).cuda().to(TDT[dtype])
+    am = [oa.argmax_first(r) for r in host(lg)]
+    lists = [am[b * (K + 1): b * (K + 1) + K - b] + ([] if b == 0 else [7]) for b in range(B)]
+    d, nd = pad(lists, K)
+    got = results(*accept_greedy(lg, d, nd, K + 1))
+    assert got == oa.greedy_round(lists, host(lg), K + 1)
+    assert am[1] == 40 * per + slab_of(V) + 1
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_stochastic_multi_slab_chunks(dtype):
+    # model drafts, B = 2, K = 2 (10 statistics rows: the narrow slabs), then an n-gram batch at V = 1.1M (wide)
+    print(f"case: stochastic multi-slab {dtype}", flush=True)
+    B, K, V = 2, 2, 300000
+    dl, tl, lists = model_case(73, B, K, V, dtype)
+    tl = torch.from_numpy(plant_second_slabs(host(tl), V, 74).astype(np.float32)).cuda().to(TDT[dtype])
+    dl = torch.from_numpy(plant_second_slabs(host(dl), V, 74).astype(np.float32)).cuda().to(TDT[dtype])
+    u, q = draw_randomness([len(x) for x in lists], V, TDT[dtype], "cuda", True,
+                           torch.Generator(device="cuda").manual_seed(75))
+    d, nd = pad(lists, K)
+    got = results(*accept_stochastic(tl, d, nd, torch.tensor([1.0, 0.8], device="cuda"), q, uniforms=u,
+                                     draft_logits=dl, target_seq_stride=K + 1, draft_seq_stride=K + 1,
+                                     draft_row_stride=1))
+    T, D, U, Q = host(tl), host(dl), u.cpu().numpy(), host(q)
+    for b, drafts in enumerate(lists):
+        k = len(drafts)
+        want = oa.verify_stochastic(drafts, T[b * (K + 1): b * (K + 1) + k + 1], D[b * (K + 1): b * (K + 1) + k],
+                                    [1.0, 0.8][b], U[b, :k], Q[b], dtype)
+        assert got[b] == want, (b, got[b], want)
+
+    K, V = 8, 1100000
+    tl = torch.from_numpy(plant_second_slabs(synth.normal(76, 77, (K + 1) * V, 2.0).reshape(K + 1, V), V, 78)
+                          .astype(np.float32)).cuda().to(TDT[dtype])
+    am = tl.argmax(-1).tolist()
+    lists = [am[:K]]
+    _, q = draw_randomness([K], V, TDT[dtype], "cuda", False, torch.Generator(device="cuda").manual_seed(79))
+    d, nd = pad(lists, K)
+    got = results(*accept_stochastic(tl, d, nd, torch.tensor([0.5], device="cuda"), q, target_seq_stride=K + 1))
+    want = oa.verify(lists[0], host(tl), None, 0.5, None, host(q)[0], dtype)
+    assert got[0] == want
+
+
+def test_sampler_multi_slab_chunks():
+    print("case: sampler multi-slab", flush=True)
+    B, V = 4, 300000
+    x = plant_second_slabs(synth.normal(80, 81, B * V, 2.0).reshape(B, V), V, 82)
+    lg = torch.from_numpy(x.astype(np.float32)).cuda().to(torch.bfloat16)
+    temps = torch.tensor([1.0, 0.0, 0.6, 1.5], device="cuda")
+    q = torch.empty(B, V, device="cuda").exponential_(1, generator=torch.Generator(device="cuda").manual_seed(83))
+    q.clamp_min_(1e-10)
+    assert sample(lg, temps, q).tolist() == oa.sample_rows(host(lg), temps.cpu().numpy(), q.cpu().numpy())
+
+
+# More drafts than 32: rows 33..63 of a sequence take lanes 33..63 of the
+# accept walks' ballots.
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_long_draft_lists(dtype):
+    print(f"case: K=40 {dtype}", flush=True)
+    B, K, V = 3, 40, 5000
+    # greedy: all 40 accepted + bonus, 37 accepted, none
+    lg = logits_tensor(90, B * (K + 1), V, dtype)
+    am = lg.argmax(-1).tolist()
+    lists = [am[0:40], am[41:41 + 37] + [(am[41 + 37] + 1) % V] + am[41 + 38:41 + 40], [(am[82] + 1) % V] * 40]
+    d, nd = pad(lists, K)
+    got = results(*accept_greedy(lg, d, nd, K + 1))
+    assert got == oa.greedy_round(lists, host(lg), K + 1)
+    assert [len(g) for g in got] == [41, 38, 1]
+    # stochastic, model drafts: identical draft and target rows accept all 40 + bonus
+    for identical in (True, False):
+        dl, tl, lists = model_case(91, B, K, V, dtype, identical)
+        u, q = draw_randomness([len(x) for x in lists], V, TDT[dtype], "cuda", True,
+                               torch.Generator(device="cuda").manual_seed(92))
+        d, nd = pad(lists, K)
+        got = results(*accept_stochastic(tl, d, nd, torch.ones(B, device="cuda"), q, uniforms=u, draft_logits=dl,
+                                         target_seq_stride=K + 1, draft_seq_stride=K + 1, draft_row_stride=1))
+        T, D, U, Q = host(tl), host(dl), u.cpu().numpy(), host(q)
+        for b, drafts in enumerate(lists):
+            k = len(drafts)
+            want = oa.verify_stochastic(drafts, T[b * (K + 1): b * (K + 1) + k + 1], D[b * (K + 1): b * (K + 1) + k],
+                                        1.0, U[b, :k], Q[b], dtype)
+            assert got[b] == want, (identical, b, got[b], want)
+        if identical:
+            assert [len(g) for g in got] == [len(x) + 1 for x in lists] and len(got[0]) == 41
+    # stochastic, n-gram drafts on peaked rows: the target samples match the drafts far past 32
+    x = synth.normal(93, 94, B * (K + 1) * V, 1.0).reshape(B * (K + 1), V)
+    peak = [int(v) for v in synth.randint(95, 96, B * (K + 1), 0, V)]
+    x[np.arange(B * (K + 1)), peak] = 40.0
+    tl = torch.from_numpy(x.astype(np.float32)).cuda().to(TDT[dtype])
+    lists = [peak[0:40], peak[41:41 + 35] + [(peak[41 + 35] + 1) % V], peak[82:82 + 12]]
+    _, q = draw_randomness([len(x) for x in lists], V, TDT[dtype], "cuda", False,
+                           torch.Generator(device="cuda").manual_seed(97))
+    d, nd = pad(lists, K)
+    got = results(*accept_stochastic(tl, d, nd, torch.tensor([1.0, 1.0, 0.9], device="cuda"), q,
+                                     target_seq_stride=K + 1))
+    T, Q = host(tl), host(q)
+    for b, drafts in enumerate(lists):
+        want = oa.verify(drafts, T[b * (K + 1): b * (K + 1) + len(drafts) + 1], None, [1.0, 1.0, 0.9][b], None,
+                         Q[b, :len(drafts) + 1], dtype)
+        assert got[b] == want, (b, got[b], want)
+    assert len(got[0]) == 41 and len(got[1]) == 36
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_accept_ratio_boundaries_multi_slab(dtype):
+    # Uniforms a hair below (accept) and above (reject) each draft's min(1, p_t/p_d), on rows whose
+    # statistics take two slabs per chunk with maxima planted in the second: every decision pins the
+    # ratio, and with it both rows' fp64 sums, to the dtype's resolution.  Call i accepts drafts
+    # 0..i-1 and rejects draft i (the last call accepts all).
+    print(f"case: ratio boundaries {dtype}", flush=True)
+    B, K, V = 3, 3, 300000
+    temps = [1.0, 0.8, 1.3]
+    T = plant_second_slabs(synth.normal(100, 101, B * (K + 1) * V, 2.0).reshape(B * (K + 1), V), V, 102)
+    D = plant_second_slabs(synth.normal(103, 104, B * K * V, 2.0).reshape(B * K, V), V, 105)
+    tl = torch.from_numpy(T.astype(np.float32)).cuda().to(TDT[dtype])
+    dl = torch.from_numpy(D.astype(np.float32)).cuda().to(TDT[dtype])
+    T, D = host(tl), host(dl)
+    floor = float(oa.round_to(1e-20, dtype))
+    lists, ratio = [], np.zeros((B, K))
+    for b in range(B):
+        pt = oa.softmax_rows(T[b * (K + 1): b * (K + 1) + K], temps[b], dtype)
+        pd = oa.softmax_rows(D[b * K: (b + 1) * K], temps[b], dtype)
+        toks = []
+        for i in range(K):
+            r = oa.div_round(pt[i], np.maximum(pd[i], floor), dtype)
+            cand = np.flatnonzero((r > 0.05) & (r < 0.95))
+            toks.append(int(cand[(7 * b + 3 * i) % len(cand)]))
+            ratio[b, i] = r[toks[-1]]
+        lists.append(toks)
+    q = torch.empty(B, V, dtype=TDT[dtype], device="cuda").exponential_(
+        1, generator=torch.Generator(device="cuda").manual_seed(106))
+    d, nd = pad(lists, K)
+    for i in range(K + 1):
+        u = np.full((B, K), 0.5, dtype=np.float32)
+        u[:, :i] = (ratio[:, :i] * (1 - 2 ** -14)).astype(np.float32)
+        if i < K:
+            u[:, i] = (ratio[:, i] * (1 + 2 ** -14)).astype(np.float32)
+        got = results(*accept_stochastic(tl, d, nd, torch.tensor(temps, device="cuda"), q,
+                                         uniforms=torch.from_numpy(u).cuda(), draft_logits=dl,
+                                         target_seq_stride=K + 1, draft_seq_stride=K, draft_row_stride=1))
+        for b in range(B):
+            want = oa.verify_stochastic(lists[b], T[b * (K + 1): (b + 1) * (K + 1)], D[b * K: (b + 1) * K],
+                                        temps[b], u[b], host(q)[b], dtype)
+            assert len(want) == i + 1
+            assert got[b] == want, (i, b, got[b], want)
