@@ -104,14 +104,31 @@ struct VerifyArgs {
 __device__ __forceinline__ u32x4 load16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 
 // A float pair as one 64-bit agent-scope (device-coherent) relaxed atomic
-// store / load: coherent across XCDs without cache maintenance instructions.
+// store: coherent across XCDs without cache maintenance instructions.
 __device__ __forceinline__ void store_agent(uint64_t* p, float x, float y) {
   const uint64_t v = (uint64_t)__float_as_uint(x) | ((uint64_t)__float_as_uint(y) << 32);
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ float2 load_agent(const uint64_t* p) {
-  const uint64_t v = __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return make_float2(__uint_as_float((uint32_t)v), __uint_as_float((uint32_t)(v >> 32)));
+
+// 16-byte stores / loads with the cache policy of the agent-scope accesses
+// above (sc1), through a buffer resource whose wave-uniform base is the
+// caller's block: one instruction per 4 floats instead of two 64-bit atomics.
+// Nothing needs them single-copy atomic: readers only load after every
+// writer's stores were acknowledged (see the merge below).
+constexpr int kCpolSc1 = 16;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t block_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+// Offsets: a per-lane byte offset plus a wave-uniform one.
+__device__ __forceinline__ void store16_agent(__amdgpu_buffer_rsrc_t r, unsigned byte_off, f32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, (int)byte_off, 0, kCpolSc1);
+}
+__device__ __forceinline__ f32x4 load16_agent(__amdgpu_buffer_rsrc_t r, unsigned byte_off, unsigned uniform_off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, (int)uniform_off, kCpolSc1));
+}
+__device__ __forceinline__ float2 load8_agent(__amdgpu_buffer_rsrc_t r, unsigned byte_off, unsigned uniform_off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)byte_off, (int)uniform_off, kCpolSc1);
+  return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
@@ -1025,31 +1042,33 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
   __syncthreads();  // also: every wave is done with its staging rows
   // every lane: the split's max over the waves for its rows, and its own
   // waves' rescale factor; wave 0 keeps the split's (max, sum) per row
+  // (every LDS read of a step is issued before the first is used: the
+  // scheduler would otherwise chain them a few at a time)
   float fac[MT];
+  float rm[MT][NW], rl[MT][NW];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) {
+      rm[mt][ww] = red_m[ww][mt * 16 + c];
+      rl[mt][ww] = w == 0 ? red_l[ww][mt * 16 + c] : 0.f;
+    }
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int m = mt * 16 + c;
-    float rm[NW];
     float M = kNegInf;
 #pragma unroll
-    for (int ww = 0; ww < NW; ++ww) {
-      rm[ww] = red_m[ww][m];
-      M = fmaxf(M, rm[ww]);
-    }
+    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, rm[mt][ww]);
     const float ref = (M == kNegInf) ? 0.f : M;
     fac[mt] = __builtin_amdgcn_exp2f((m_run[mt] - ref) * sc);
     if (w == 0 && g4 == 0) {
       float L = 0.f;
 #pragma unroll
-      for (int ww = 0; ww < NW; ++ww) L = fmaf(red_l[ww][m], __builtin_amdgcn_exp2f((rm[ww] - ref) * sc), L);
+      for (int ww = 0; ww < NW; ++ww) L = fmaf(rl[mt][ww], __builtin_amdgcn_exp2f((rm[mt][ww] - ref) * sc), L);
       const float ms = M == kNegInf ? kNegInf : M * sc;  // partials carry the log2-domain max
       row_ms[m] = ms;
       row_l[m] = L;
-      if (nsplit > 1 && m < a.Mv) {
-        const bool real = row_pos[m] >= 0;
-        store_agent(reinterpret_cast<uint64_t*>(&a.part_ml[(((int64_t)pair * a.S + split) * a.Mv + m) * 2]),
-                    real ? ms : kNegInf, real ? L : 0.f);
-      }
     }
   }
   // Every wave's scaled O rows (real rows only: rows >= Mv are padding) go
@@ -1062,6 +1081,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
   constexpr int ITEMS = (MROWS * C4 + NT - 1) / NT;
   f32x4 own[MPASS][ITEMS];
   const int64_t pbase = ((int64_t)pair * a.S + split) * a.Mv;
+  const __amdgpu_buffer_rsrc_t prs = block_rsrc(a.part_o + pbase * DH);  // this split's partial rows
 #pragma unroll
   for (int ps = 0; ps < MPASS; ++ps) {
     if (ps > 0) __syncthreads();  // the previous pass fully read
@@ -1077,6 +1097,14 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
       }
     }
     __syncthreads();
+    f32x4 wv[ITEMS][NW];
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+      const int r = min((tid + j * NT) / C4, MROWS - 1), c4 = (tid + j * NT) % C4;  // rows past MROWS: discarded
+#pragma unroll
+      for (int ww = 0; ww < NW; ++ww) wv[j][ww] = *reinterpret_cast<const f32x4*>(&region[(ww * MROWS + r) * RSTR + c4 * 4]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int j = 0; j < ITEMS; ++j) {
       const int qd = tid + j * NT;
@@ -1084,9 +1112,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
       const int m = ps * MROWS + r;
       own[ps][j] = f32x4{0.f, 0.f, 0.f, 0.f};
       if (r >= MROWS || m >= a.Mv) continue;
-      f32x4 o = *reinterpret_cast<const f32x4*>(&region[r * RSTR + c4 * 4]);
+      f32x4 o = wv[j][0];
 #pragma unroll
-      for (int ww = 1; ww < NW; ++ww) o += *reinterpret_cast<const f32x4*>(&region[(ww * MROWS + r) * RSTR + c4 * 4]);
+      for (int ww = 1; ww < NW; ++ww) o += wv[j][ww];
       if (row_pos[m] < 0) o = f32x4{0.f, 0.f, 0.f, 0.f};
       own[ps][j] = o;
       if (nsplit == 1) {
@@ -1099,22 +1127,55 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
         const uint32_t hi = (uint32_t)f32_to_bf16_bits(o[2] * inv) | ((uint32_t)f32_to_bf16_bits(o[3] * inv) << 16);
         *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
       } else {
-        uint64_t* dst = reinterpret_cast<uint64_t*>(&a.part_o[(pbase + m) * DH + c4 * 4]);
-        store_agent(dst, o[0], o[1]);
-        store_agent(dst + 1, o[2], o[3]);
+        store16_agent(prs, (unsigned)(m * DH + c4 * 4) * 4u, o);
       }
     }
   }
   if (nsplit == 1) return;
+  // the split's (max, sum) per row, written by wave 0 before the barrier above
+  // (stored only now, so that barrier did not wait for the store's acknowledgement)
+  if (tid < a.Mv) {
+    const bool real = row_pos[tid] >= 0;
+    store_agent(reinterpret_cast<uint64_t*>(&a.part_ml[(pbase + tid) * 2]), real ? row_ms[tid] : kNegInf,
+                real ? row_l[tid] : 0.f);
+  }
+  // What the merge needs of this thread's items that no other split holds
+  // (validity, offsets, destination, this split's (max, sum)), computed while
+  // the stores above are acknowledged and the arrival atomic is in flight:
+  // the last split's merge is a chain of single-wave instructions, so every
+  // instruction taken off it shortens the kernel.
+  bool iok[MPASS][ITEMS];
+  unsigned ioff[MPASS][ITEMS], imlo[MPASS][ITEMS];  // byte offsets in a split's partial rows / (max, sum) pairs
+  float ims[MPASS][ITEMS], ils[MPASS][ITEMS];
+  uint2* idst[MPASS][ITEMS];
+#pragma unroll
+  for (int ps = 0; ps < MPASS; ++ps)
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+      const int qd = tid + j * NT;
+      const int r = qd / C4, c4 = qd % C4;
+      int m = ps * MROWS + r;
+      const int g = m / a.QL, t = m - g * a.QL;
+      const bool ok = r < MROWS && m < a.Mv && t < qlen;
+      iok[ps][j] = ok;
+      m = ok ? m : 0;
+      ioff[ps][j] = (unsigned)(m * DH + c4 * 4) * 4u;
+      imlo[ps][j] = (unsigned)m * 8u;
+      const bool real = row_pos[m] >= 0;
+      ims[ps][j] = real ? row_ms[m] : kNegInf;
+      ils[ps][j] = real ? row_l[m] : 0.f;
+      idst[ps][j] = reinterpret_cast<uint2*>(
+          (bf16_t*)a.out + ((int64_t)(q0 + (ok ? t : 0)) * a.H + hk * a.Gs + a.g0 + (ok ? g : 0)) * DH + c4 * 4);
+    }
 
   // ---- cross-split merge by the pair's last split to finish ------------------
   // Ordering without release/acquire (which on gfx950 would write back and
   // invalidate whole L2s: 45 us per call measured): the partials above and
-  // the (max, sum) pairs are agent-scope relaxed atomic stores (sc1: written
-  // through to the device's point of coherence).  Every thread waits for
+  // the (max, sum) pairs are stored with sc1 (agent scope: written through to
+  // the device's point of coherence).  Every thread waits for
   // their acknowledgement (vmcnt(0)) before the barrier that precedes the
-  // arrival atomic; the split that counts last issues its agent-scope loads
-  // (served from the point of coherence, past any cached copy) only after
+  // arrival atomic; the split that counts last issues its sc1 loads (served
+  // from the point of coherence, past any cached copy) only after
   // the counter's value came back, so it reads every other split's partials.
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
@@ -1125,78 +1186,85 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
   __syncthreads();
   if (!is_last) return;
   if (tid == 0) __hip_atomic_store(&a.counters[counter_slot(pair)], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  // The other splits' partials and (max, sum) pairs for this thread's items,
-  // loaded CH splits per round trip (all loads of a round trip issued before
-  // any is used); this split's own sums are still in registers.
   const int64_t base0 = (int64_t)pair * a.S * a.Mv;  // row 0 of split 0
-  constexpr int CH = 4;
-  // Up to CH splits: every value this thread merges, for all its items,
-  // is loaded in one round trip (all loads issued before any is used).
-  // Splits fold in a fixed order (0, 1, ...), whichever split merges, so
-  // the result does not depend on which split finished last.
+  const __amdgpu_buffer_rsrc_t ors = block_rsrc(a.part_o + base0 * DH);   // the pair's partial rows
+  const __amdgpu_buffer_rsrc_t mrs = block_rsrc(a.part_ml + base0 * 2);   // and (max, sum) pairs
+  constexpr int CH = 4;  // splits whose values one round trip loads
+  // Splits combine in a fixed order (0, 1, ...), whichever split merges, so
+  // the result does not depend on which split finished last.  A row with no
+  // key so far (max -inf) takes reference 0, so its weights are exactly 0.
   auto fold = [&](float& M, float& den, f32x4& num, float ms, float ls, f32x4 os) {
     const float Mn = fmaxf(M, ms);
-    if (Mn == kNegInf) return;  // no key of this row so far
-    const float a0 = exp2f(M - Mn), a1 = exp2f(ms - Mn);  // -inf: 0
+    const float ref = Mn == kNegInf ? 0.f : Mn;
+    const float a0 = __builtin_amdgcn_exp2f(M - ref), a1 = __builtin_amdgcn_exp2f(ms - ref);
     den = den * a0 + ls * a1;
     num = num * a0 + os * a1;
     M = Mn;
   };
-  auto write_out = [&](int m, int c4, float den, f32x4 num) {
-    const int g = m / a.QL, t = m - g * a.QL;
+  auto emit = [&](uint2* dst, float den, f32x4 num) {
     const float inv = den > 0.f ? 1.f / den : 0.f;
-    bf16_t* dst = (bf16_t*)a.out + ((int64_t)(q0 + t) * a.H + hk * a.Gs + a.g0 + g) * DH + c4 * 4;
     const uint32_t lo = (uint32_t)f32_to_bf16_bits(num[0] * inv) | ((uint32_t)f32_to_bf16_bits(num[1] * inv) << 16);
     const uint32_t hi = (uint32_t)f32_to_bf16_bits(num[2] * inv) | ((uint32_t)f32_to_bf16_bits(num[3] * inv) << 16);
-    *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
+    *dst = make_uint2(lo, hi);
   };
-  auto item_ok = [&](int ps, int j, int& m, int& c4) {
-    const int qd = tid + j * NT;
-    const int r = qd / C4;
-    c4 = qd % C4;
-    m = ps * MROWS + r;
-    if (r >= MROWS || m >= a.Mv) return false;
-    return m - (m / a.QL) * a.QL < qlen;
-  };
+  // a real split other than this one (its values are loaded and not used)
+  auto other = [&](int sp) { return (sp < nsplit && sp != split) ? sp : (split == 0 ? 1 : 0); };
   if (nsplit <= CH) {
-    float2 ml[MPASS][ITEMS][CH], o01[MPASS][ITEMS][CH], o23[MPASS][ITEMS][CH];
+    // every value this thread merges, for all its items, in one round trip
+    // (items past the rows load row 0 and are discarded)
+    float2 ml[MPASS][ITEMS][CH];
+    f32x4 op[MPASS][ITEMS][CH];
+#pragma unroll
+    for (int k = 0; k < CH; ++k) {
+      const unsigned rows = (unsigned)(other(k) * a.Mv);
+#pragma unroll
+      for (int ps = 0; ps < MPASS; ++ps)
+#pragma unroll
+        for (int j = 0; j < ITEMS; ++j) {
+          ml[ps][j][k] = load8_agent(mrs, imlo[ps][j], rows * 8u);
+          op[ps][j][k] = load16_agent(ors, ioff[ps][j], rows * (DH * 4u));
+        }
+    }
+    // every item is folded before the first output store: on gfx9 one
+    // counter tracks loads and stores, so a load waited for after a store
+    // would also wait for the store's acknowledgement
+    // (one maximum over the splits, then one weight per split: splits past
+    // nsplit weigh 0, this split's own values come from registers)
+    float dens[MPASS][ITEMS];
+    f32x4 nums[MPASS][ITEMS];
 #pragma unroll
     for (int ps = 0; ps < MPASS; ++ps)
 #pragma unroll
       for (int j = 0; j < ITEMS; ++j) {
-        int m, c4;
-        const bool ok = item_ok(ps, j, m, c4);
-        m = ok ? m : 0;
+        float ms[CH], ls[CH];
+        f32x4 os[CH];
+        float M = kNegInf;
 #pragma unroll
         for (int k = 0; k < CH; ++k) {
-          const int sp = (k < nsplit && k != split) ? k : (split == 0 ? 1 : 0);  // a real split (not used below)
-          const int64_t rr = base0 + (int64_t)sp * a.Mv + m;
-          if (ok) {
-            ml[ps][j][k] = load_agent(reinterpret_cast<const uint64_t*>(&a.part_ml[rr * 2]));
-            o01[ps][j][k] = load_agent(reinterpret_cast<const uint64_t*>(&a.part_o[rr * DH + c4 * 4]));
-            o23[ps][j][k] = load_agent(reinterpret_cast<const uint64_t*>(&a.part_o[rr * DH + c4 * 4 + 2]));
-          }
+          const bool mine = k == split, used = k < nsplit;
+          ms[k] = !used ? kNegInf : (mine ? ims[ps][j] : ml[ps][j][k].x);
+          ls[k] = !used ? 0.f : (mine ? ils[ps][j] : ml[ps][j][k].y);
+          os[k] = !used ? f32x4{0.f, 0.f, 0.f, 0.f} : (mine ? own[ps][j] : op[ps][j][k]);
+          M = fmaxf(M, ms[k]);
         }
-      }
-#pragma unroll
-    for (int ps = 0; ps < MPASS; ++ps)
-#pragma unroll
-      for (int j = 0; j < ITEMS; ++j) {
-        int m, c4;
-        if (!item_ok(ps, j, m, c4)) continue;
-        float M = kNegInf, den = 0.f;
+        const float ref = M == kNegInf ? 0.f : M;
+        float den = 0.f;
         f32x4 num = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int k = 0; k < CH; ++k) {
-          if (k >= nsplit) break;
-          if (k == split)
-            fold(M, den, num, row_pos[m] >= 0 ? row_ms[m] : kNegInf, row_pos[m] >= 0 ? row_l[m] : 0.f, own[ps][j]);
-          else
-            fold(M, den, num, ml[ps][j][k].x, ml[ps][j][k].y,
-                 f32x4{o01[ps][j][k].x, o01[ps][j][k].y, o23[ps][j][k].x, o23[ps][j][k].y});
+          const float wk = __builtin_amdgcn_exp2f(ms[k] - ref);  // -inf: 0
+          den = fmaf(ls[k], wk, den);
+          num += os[k] * wk;
         }
-        write_out(m, c4, den, num);
+        dens[ps][j] = den;
+        nums[ps][j] = num;
       }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int ps = 0; ps < MPASS; ++ps)
+#pragma unroll
+      for (int j = 0; j < ITEMS; ++j)
+        if (iok[ps][j]) emit(idst[ps][j], dens[ps][j], nums[ps][j]);
     return;
   }
   // more splits: CH per round trip
@@ -1204,32 +1272,27 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
   for (int ps = 0; ps < MPASS; ++ps) {
 #pragma unroll
     for (int j = 0; j < ITEMS; ++j) {
-      int m, c4;
-      if (!item_ok(ps, j, m, c4)) continue;
+      if (!iok[ps][j]) continue;
       float M = kNegInf, den = 0.f;
       f32x4 num = f32x4{0.f, 0.f, 0.f, 0.f};
       for (int s0 = 0; s0 < nsplit; s0 += CH) {
-        float2 ml[CH], o01[CH], o23[CH];
+        float2 ml[CH];
+        f32x4 op[CH];
 #pragma unroll
         for (int k = 0; k < CH; ++k) {
-          int sp = s0 + k;
-          sp = (sp < nsplit && sp != split) ? sp : (split == 0 ? 1 : 0);  // a real split (not used below)
-          const int64_t rr = base0 + (int64_t)sp * a.Mv + m;
-          ml[k] = load_agent(reinterpret_cast<const uint64_t*>(&a.part_ml[rr * 2]));
-          o01[k] = load_agent(reinterpret_cast<const uint64_t*>(&a.part_o[rr * DH + c4 * 4]));
-          o23[k] = load_agent(reinterpret_cast<const uint64_t*>(&a.part_o[rr * DH + c4 * 4 + 2]));
+          const unsigned rows = (unsigned)(other(s0 + k) * a.Mv);
+          ml[k] = load8_agent(mrs, imlo[ps][j], rows * 8u);
+          op[k] = load16_agent(ors, ioff[ps][j], rows * (DH * 4u));
         }
 #pragma unroll
         for (int k = 0; k < CH; ++k) {
           const int sp = s0 + k;
           if (sp >= nsplit) break;
-          if (sp == split)
-            fold(M, den, num, row_pos[m] >= 0 ? row_ms[m] : kNegInf, row_pos[m] >= 0 ? row_l[m] : 0.f, own[ps][j]);
-          else
-            fold(M, den, num, ml[k].x, ml[k].y, f32x4{o01[k].x, o01[k].y, o23[k].x, o23[k].y});
+          if (sp == split) fold(M, den, num, ims[ps][j], ils[ps][j], own[ps][j]);
+          else fold(M, den, num, ml[k].x, ml[k].y, op[k]);
         }
       }
-      write_out(m, c4, den, num);
+      emit(idst[ps][j], den, num);
     }
   }
 }
