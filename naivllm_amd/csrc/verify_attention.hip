@@ -28,7 +28,9 @@
 
 #include "common.h"
 
+#include <algorithm>
 #include <mutex>
+#include <type_traits>
 
 namespace {
 
@@ -1189,7 +1191,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
   const int64_t base0 = (int64_t)pair * a.S * a.Mv;  // row 0 of split 0
   const __amdgpu_buffer_rsrc_t ors = block_rsrc(a.part_o + base0 * DH);   // the pair's partial rows
   const __amdgpu_buffer_rsrc_t mrs = block_rsrc(a.part_ml + base0 * 2);   // and (max, sum) pairs
-  constexpr int CH = 4;  // splits whose values one round trip loads
+  constexpr int CH = 4;  // beyond 8 splits: splits whose values one round trip loads
   // Splits combine in a fixed order (0, 1, ...), whichever split merges, so
   // the result does not depend on which split finished last.  A row with no
   // key so far (max -inf) takes reference 0, so its weights are exactly 0.
@@ -1209,13 +1211,14 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
   };
   // a real split other than this one (its values are loaded and not used)
   auto other = [&](int sp) { return (sp < nsplit && sp != split) ? sp : (split == 0 ? 1 : 0); };
-  if (nsplit <= CH) {
-    // every value this thread merges, for all its items, in one round trip
-    // (items past the rows load row 0 and are discarded)
-    float2 ml[MPASS][ITEMS][CH];
-    f32x4 op[MPASS][ITEMS][CH];
+  // Up to 8 splits: every value this thread merges, for all its items, in
+  // one round trip (items past the rows load row 0 and are discarded).
+  auto merge_in_one_trip = [&](auto width) {
+    constexpr int CW = decltype(width)::value;
+    float2 ml[MPASS][ITEMS][CW];
+    f32x4 op[MPASS][ITEMS][CW];
 #pragma unroll
-    for (int k = 0; k < CH; ++k) {
+    for (int k = 0; k < CW; ++k) {
       const unsigned rows = (unsigned)(other(k) * a.Mv);
 #pragma unroll
       for (int ps = 0; ps < MPASS; ++ps)
@@ -1225,22 +1228,22 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
           op[ps][j][k] = load16_agent(ors, ioff[ps][j], rows * (DH * 4u));
         }
     }
-    // every item is folded before the first output store: on gfx9 one
+    // every item is combined before the first output store: on gfx9 one
     // counter tracks loads and stores, so a load waited for after a store
-    // would also wait for the store's acknowledgement
-    // (one maximum over the splits, then one weight per split: splits past
-    // nsplit weigh 0, this split's own values come from registers)
+    // would also wait for the store's acknowledgement.  (One maximum over
+    // the splits, then one weight per split: splits past nsplit weigh 0,
+    // this split's own values come from registers.)
     float dens[MPASS][ITEMS];
     f32x4 nums[MPASS][ITEMS];
 #pragma unroll
     for (int ps = 0; ps < MPASS; ++ps)
 #pragma unroll
       for (int j = 0; j < ITEMS; ++j) {
-        float ms[CH], ls[CH];
-        f32x4 os[CH];
+        float ms[CW], ls[CW];
+        f32x4 os[CW];
         float M = kNegInf;
 #pragma unroll
-        for (int k = 0; k < CH; ++k) {
+        for (int k = 0; k < CW; ++k) {
           const bool mine = k == split, used = k < nsplit;
           ms[k] = !used ? kNegInf : (mine ? ims[ps][j] : ml[ps][j][k].x);
           ls[k] = !used ? 0.f : (mine ? ils[ps][j] : ml[ps][j][k].y);
@@ -1251,7 +1254,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
         float den = 0.f;
         f32x4 num = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int k = 0; k < CH; ++k) {
+        for (int k = 0; k < CW; ++k) {
           const float wk = __builtin_amdgcn_exp2f(ms[k] - ref);  // -inf: 0
           den = fmaf(ls[k], wk, den);
           num += os[k] * wk;
@@ -1265,6 +1268,13 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
 #pragma unroll
       for (int j = 0; j < ITEMS; ++j)
         if (iok[ps][j]) emit(idst[ps][j], dens[ps][j], nums[ps][j]);
+  };
+  if (nsplit <= 4) {
+    merge_in_one_trip(std::integral_constant<int, 4>{});
+    return;
+  }
+  if (nsplit <= 8) {
+    merge_in_one_trip(std::integral_constant<int, 8>{});
     return;
   }
   // more splits: CH per round trip
@@ -1581,25 +1591,29 @@ int make_plan(int B, int H, int Hkv, int D, int block_size, int max_blocks, int 
   // pair's K through every slice's L1, whose fill rate (~25 GB/s per CU)
   // then bounds it.  Measured on MI355X (Qwen3-0.6B layer, ~1.25k keys,
   // graph-replayed over 28 pools; d-sliced with its merge launch against
-  // the best key split): 8 pairs 11.0 against 12.4 us, 16 pairs 12.7
-  // against 13.3, 32 pairs 16.2 against 14.7, 64 pairs 17.2 against 17.0;
-  // at 128 pairs x 16k-32k keys the key-split kernel is 2x faster.  So
-  // key-split from a quarter as many pairs as resident workgroups, or when
-  // a table holds >= 4096 keys.
+  // the best key split): 8 pairs 11.1 against 11.5 us, 16 pairs 12.7
+  // against 12.0, 32 pairs 14.4 (d-sliced: 16.2) against 13.3, 64 pairs
+  // 17.2 against 16.8; at 128 pairs x 16k-32k keys the key-split kernel is
+  // 2x faster.  So key-split from a sixteenth as many pairs as resident
+  // workgroups, or when a table holds >= 4096 keys.
   const int64_t ks_slots = (int64_t)cus * (8 / kKsWaves);  // resident workgroups
   const bool ks_fits = p->MT <= 3 && block_size >= 16 && max_blocks <= kMaxSplitPages &&
                        (pairs <= kMaxCounterPairs || (kv_split_tokens == 0 && pairs >= ks_slots));
-  const bool ks_wins = kv_split_tokens > 0 || pairs * 8 >= ks_slots || max_ctx >= 4096;
+  const bool ks_wins = kv_split_tokens > 0 || pairs * 16 >= ks_slots || max_ctx >= 4096;
   if (dtype == NSV_BF16 && ks_fits && ks_wins) {
     // key-split kernel: each sequence's keys evenly over about CUs / pairs
     // splits (none when the pairs alone cover the chip), but no split
-    // shorter than 256 keys (two tiles per wave: shorter splits pay the
-    // merge for too few loads; at 32 pairs x 1.25k keys, 10 splits take
-    // 21.0 us against 14.7 for 5), or the caller's fixed split length
+    // shorter than 160 keys (shorter splits pay the merge for too few loads:
+    // at 8 pairs x 1.25k keys, 8 splits take 11.5 us, 10 12.7, 16 12.7; at
+    // 32 pairs 8 take 13.3 against 14.4 for 5), or the caller's fixed split
+    // length
     p->ks = 1;
     if (split == 0) {
       int64_t S = pairs > 0 ? (ks_slots + pairs / 2) / pairs : 1;
-      const int64_t max_splits = (max_ctx + 255) / 256;
+      // (merges of more than 8 splits take more than one round trip: those
+      // splits are at least 512 keys long)
+      int64_t max_splits = (max_ctx + 159) / 160;
+      if (max_splits > 8) max_splits = std::max<int64_t>(8, (max_ctx + 511) / 512);
       if (S > max_splits) S = max_splits;
       if (S > 64) S = 64;
       if (S < 1 || pairs > kMaxCounterPairs) S = 1;

@@ -68,18 +68,23 @@ def test_workspace_size_matches_split_plan():
     # pairs x 4 key splits fill the 256 CUs a host without a GPU assumes
     rows = 8 * 8 * 4 * 18
     assert h.nsv_verify_attention_workspace_size(8, 16, 8, 128, 256, 6, 9, 1, 0) == cnt + pad(rows * 8) + rows * 512
-    # 4 sequences: 32 pairs take the key-split kernel too, 8 splits each by the CU count but
-    # none shorter than 256 keys: 6 for the 1536-key tables
+    # 4 sequences: 32 pairs take the key-split kernel too, 8 splits each by the CU count (none
+    # shorter than 160 keys)
     import ctypes
     kind, splits = ctypes.c_int(), ctypes.c_int()
     assert h.nsv_verify_attention_plan(4, 16, 8, 128, 256, 6, 9, 1, 0, 256, ctypes.addressof(kind),
                                        ctypes.addressof(splits)) == 0
-    assert (kind.value, splits.value) == (1, 6)
-    rows = 4 * 8 * 6 * 18
+    assert (kind.value, splits.value) == (1, 8)
+    rows = 4 * 8 * 8 * 18
     assert h.nsv_verify_attention_workspace_size(4, 16, 8, 128, 256, 6, 9, 1, 0) == cnt + pad(rows * 8) + rows * 512
-    # 2 sequences: 16 pairs keep the d-sliced kernel (4 head-dim slices, key splits merged by a
-    # second kernel)
+    # 2 sequences: 16 pairs take it as well; the CU count asks 16 splits, but more than 8 need
+    # 512-key splits: 8
     assert h.nsv_verify_attention_plan(2, 16, 8, 128, 256, 6, 9, 1, 0, 256, ctypes.addressof(kind),
+                                       ctypes.addressof(splits)) == 0
+    assert (kind.value, splits.value) == (1, 8)
+    # 1 sequence: 8 pairs keep the d-sliced kernel (4 head-dim slices, key splits merged by a
+    # second kernel)
+    assert h.nsv_verify_attention_plan(1, 16, 8, 128, 256, 6, 9, 1, 0, 256, ctypes.addressof(kind),
                                        ctypes.addressof(splits)) == 0
     assert kind.value == 0
     # 16-page tables (4096 keys): the key-split kernel, 4 splits per sequence for 64 pairs on
@@ -105,8 +110,9 @@ def test_plan_serves_large_groups_in_head_subsets():
     for H, mq in [(32, 17), (64, 9), (64, 33), (8, 64)]:
         assert h.nsv_verify_attention_plan(2, H, 8, 128, 256, 24, mq, 1, 0, 256, ctypes.addressof(kind),
                                            ctypes.addressof(splits)) == 0, (H, mq)
-    # GQA-4 x 17 rows: 2 heads (34 rows) per launch; 24-page tables -> key-split, 16 splits for 16 pairs
-    rows = 2 * 8 * 16 * 34
+    # GQA-4 x 17 rows: 2 heads (34 rows) per launch; 24-page tables -> key-split, 16 splits asked
+    # for 16 pairs, 12 of at least 512 keys
+    rows = 2 * 8 * 12 * 34
     pad = lambda x: (x + 255) // 256 * 256
     assert h.nsv_verify_attention_workspace_size(2, 32, 8, 128, 256, 24, 17, 1, 0) == 65536 + pad(rows * 8) + rows * 512
 

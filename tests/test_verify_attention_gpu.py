@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 import torch
 
-from naivllm_amd.layers.attention import paged_attention_verify, store_kvcache
+from naivllm_amd.layers.attention import paged_attention_verify, store_kvcache, verify_attention_plan
 from naivllm_amd.utils import synth
 from oracle import attention as ora
 from tests.gpu_util import assert_close, to_device
@@ -20,6 +20,13 @@ def _gpu(vb, block_m=16, **kw):
                                  vb.num_kv_heads, vb.head_dim, vb.block_size, block_m, **kw)
     torch.cuda.synchronize()
     return out
+
+
+def _kernel(vb, max_q_len):
+    """The kernel the plan runs for this batch on the current device."""
+    dtype = torch.float32 if vb.dtype == "f32" else torch.bfloat16
+    return verify_attention_plan(len(vb.context_lens), vb.num_heads, vb.num_kv_heads, vb.head_dim, vb.block_size,
+                                 vb.block_tables.shape[1], max_q_len, dtype)[0]
 
 
 def _oracle(vb):
@@ -54,40 +61,47 @@ def test_split_sizes_agree_with_oracle(dtype, split):
     assert_close(out, _oracle(vb), dtype, f"split {split}")
 
 
-@pytest.mark.parametrize("dtype,max_blocks", [("bf16", None), ("f32", None), ("bf16", 24)])
-def test_gqa4_8b_shape(dtype, max_blocks):
-    # 36 rows of the 4-head group: three 16-row m-tiles (d-sliced kernel for
-    # the 6-page table, key-split kernel for the 24-page one)
-    print(f"case: 32Q/8KV dtype={dtype} max_blocks={max_blocks}", flush=True)
-    vb = synth.verify_batch(22, [900, 1500], [9, 9], num_heads=32, num_kv_heads=8, dtype=dtype,
-                            max_blocks=max_blocks)
+@pytest.mark.parametrize("dtype,ctx,max_blocks,kernel", [("bf16", [1500], None, "d-sliced"), ("f32", [900, 1500], None, "fp32"),
+                                                        ("bf16", [900, 1500], None, "key-split"),
+                                                        ("bf16", [900, 1500], 24, "key-split")])
+def test_gqa4_8b_shape(dtype, ctx, max_blocks, kernel):
+    # 36 rows of the 4-head group: three 16-row m-tiles (one sequence's 8
+    # pairs take the d-sliced kernel, two sequences the key-split kernel)
+    print(f"case: 32Q/8KV dtype={dtype} ctx={ctx} max_blocks={max_blocks}", flush=True)
+    vb = synth.verify_batch(22, ctx, [9] * len(ctx), num_heads=32, num_kv_heads=8, dtype=dtype, max_blocks=max_blocks)
+    assert _kernel(vb, 9) == kernel
     out = _gpu(vb, max_q_len=9)
     assert_close(out, _oracle(vb), dtype, "gqa4")
 
 
-@pytest.mark.parametrize("dtype,max_blocks,H,ql", [("bf16", None, 32, 17), ("bf16", 24, 32, 17), ("f32", None, 32, 17),
-                                                   ("bf16", None, 64, 9), ("bf16", 24, 64, 9), ("f32", None, 64, 9)])
-def test_groups_beyond_64_rows(dtype, max_blocks, H, ql):
+@pytest.mark.parametrize("dtype,max_blocks,G,ql,Hkv,kernel",
+                         [("bf16", None, 4, 17, 4, "d-sliced"), ("bf16", 24, 4, 17, 8, "key-split"),
+                          ("f32", None, 4, 17, 8, "fp32"), ("bf16", None, 8, 9, 4, "d-sliced"),
+                          ("bf16", 24, 8, 9, 8, "key-split"), ("f32", None, 8, 9, 8, "fp32")])
+def test_groups_beyond_64_rows(dtype, max_blocks, G, ql, Hkv, kernel):
     # (H / Hkv) * max_q_len > 64 rows: GQA-4 with K = 16 drafts (68 rows)
     # and GQA-8 with K = 8 (72 rows) run as launches over subsets of each
     # kv head's query heads (2 of 4, 4 of 8), through the d-sliced kernel
-    # (6-page tables), the key-split kernel (24 pages) and the fp32 kernel;
-    # the second sequence is ragged and carries padding rows
-    print(f"case: {H}Q/8KV {ql} rows per sequence, dtype={dtype} max_blocks={max_blocks}", flush=True)
-    vb = synth.verify_batch(23, [1100, 1500], [ql, ql - 3], num_heads=H, num_kv_heads=8, dtype=dtype,
+    # (8 pairs), the key-split kernel and the fp32 kernel; the second
+    # sequence is ragged and carries padding rows
+    print(f"case: {G * Hkv}Q/{Hkv}KV {ql} rows per sequence, dtype={dtype} max_blocks={max_blocks}", flush=True)
+    vb = synth.verify_batch(23, [1100, 1500], [ql, ql - 3], num_heads=G * Hkv, num_kv_heads=Hkv, dtype=dtype,
                             max_blocks=max_blocks, pad_rows=[0, 2])
+    assert _kernel(vb, ql) == kernel
     out = _gpu(vb, max_q_len=ql)
-    assert_close(out, _oracle(vb), dtype, f"{H // 8} heads x {ql} rows")
+    assert_close(out, _oracle(vb), dtype, f"{G} heads x {ql} rows")
 
 
-@pytest.mark.parametrize("max_blocks", [None, 16])
-def test_small_batch_many_key_splits(max_blocks):
-    # few (sequence, kv head) pairs: each context is cut into many short
-    # splits (some sequences shorter than one split per CU share); a 5-page
-    # table takes the d-sliced kernel and its merge kernel, a 16-page table
-    # (4096 keys) the key-split kernel and its in-kernel merge
+@pytest.mark.parametrize("max_blocks,kernel", [(None, "d-sliced"), (16, "key-split")])
+def test_small_batch_many_key_splits(max_blocks, kernel):
+    # few (sequence, kv head) pairs (4 x 2): each context is cut into many
+    # short splits (some sequences shorter than one split per CU share); a
+    # 5-page table takes the d-sliced kernel and its merge kernel, a 16-page
+    # table (4096 keys) the key-split kernel and its in-kernel merge
     print(f"case: b4 bf16 short and long contexts, max_blocks={max_blocks}", flush=True)
-    vb = synth.verify_batch(27, [1, 17, 300, 1248], [1, 9, 9, 9], dtype="bf16", max_blocks=max_blocks)
+    vb = synth.verify_batch(27, [1, 17, 300, 1248], [1, 9, 9, 9], num_heads=4, num_kv_heads=2, dtype="bf16",
+                            max_blocks=max_blocks)
+    assert _kernel(vb, 9) == kernel
     out = _gpu(vb, max_q_len=9)
     assert_close(out, _oracle(vb), "bf16", "many splits")
 
@@ -106,13 +120,17 @@ def test_workspace_reuse_across_shapes():
         assert_close(out, _oracle(vb), "bf16", f"reuse b{batch}")
 
 
-@pytest.mark.parametrize("batch,bs,qlen", [(16, 256, 9), (32, 16, 9), (20, 64, 5)])
-def test_wide_batches_use_64_dim_slices(batch, bs, qlen):
-    # >= 128 (sequence, kv head) pairs fill the chip with two 64-dim slices
-    # per pair (the 32-dim slicing of smaller batches is covered above)
+@pytest.mark.parametrize("batch,bs,qlen,kernel", [(16, 256, 9, "key-split"), (32, 16, 9, "key-split"),
+                                                 (20, 64, 5, "key-split"), (16, 8, 9, "d-sliced")])
+def test_wide_batches(batch, bs, qlen, kernel):
+    # >= 128 (sequence, kv head) pairs: the key-split kernel with one split
+    # per pair; pages below 16 keys take the d-sliced kernel, which fills the
+    # chip with two 64-dim slices per pair (the 32-dim slicing of smaller
+    # batches is covered above)
     print(f"case: wide batch={batch} block_size={bs} q_len={qlen}", flush=True)
     ctx = [int(x) for x in synth.randint(26, batch, batch, 40, 700)]
     vb = synth.verify_batch(26 + batch, ctx, [qlen] * batch, block_size=bs, dtype="bf16")
+    assert _kernel(vb, qlen) == kernel
     out = _gpu(vb, max_q_len=qlen)
     assert_close(out, _oracle(vb), "bf16", f"wide b{batch}")
 
