@@ -134,6 +134,15 @@ __device__ __forceinline__ void head_norm_rope(float x1, float x2, float inv, fl
   o2 = f32_to_bf16_bits(y1 * s + y2 * c);
 }
 
+// Workgroup barrier that orders LDS accesses only: unlike __syncthreads() it
+// does not wait for the wave's outstanding global loads, so a load pipeline
+// issued before it stays in flight.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 static inline int nsv_launch_status() {
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? NSV_OK : (int)e;

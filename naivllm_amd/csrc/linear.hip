@@ -150,15 +150,22 @@ __global__ __launch_bounds__(kLinThreads, lin_waves_per_eu(MT, SMALL, BNV)) void
     u32x4 xv[AL];  // activation rows rr + RPI j
     u32x4 nv;      // RMSNorm weight
     int k0;
+    bool in;       // this lane's 8 elements lie inside the reduction
   };
   const u32x4 zero4 = {0u, 0u, 0u, 0u};
+  // Every issue has the same loads, unconditionally (lanes past K read
+  // elements 0.. and their values are replaced by zeros when staged): loads
+  // under a branch leave the compiler unable to count them, and it then
+  // waits for every load in flight, the next chunk's included, before a
+  // chunk is multiplied.
   auto issue = [&](Chunk& ch, int k0) {
-    const bool in = k0 + KC <= K || k0 + cc * 8 < K;
+    ch.in = k0 + KC <= K || k0 + cc * 8 < K;
+    const int kk = ch.in ? k0 : -cc * 8;
 #pragma unroll
-    for (int j = 0; j < WL; ++j) ch.wv[j] = in ? *reinterpret_cast<const u32x4*>(wp[j] + k0) : zero4;
+    for (int j = 0; j < WL; ++j) ch.wv[j] = *reinterpret_cast<const u32x4*>(wp[j] + kk);
 #pragma unroll
-    for (int j = 0; j < AL; ++j) ch.xv[j] = in ? *reinterpret_cast<const u32x4*>(xp[j] + k0) : zero4;
-    if constexpr (NORM) ch.nv = in ? *reinterpret_cast<const u32x4*>(a.norm_w + k0 + cc * 8) : zero4;
+    for (int j = 0; j < AL; ++j) ch.xv[j] = *reinterpret_cast<const u32x4*>(xp[j] + kk);
+    if constexpr (NORM) ch.nv = *reinterpret_cast<const u32x4*>(a.norm_w + kk + cc * 8);
     ch.k0 = k0;
   };
 
@@ -180,7 +187,7 @@ __global__ __launch_bounds__(kLinThreads, lin_waves_per_eu(MT, SMALL, BNV)) void
     // chunk instead of every activation row.
 #pragma unroll
     for (int j = 0; j < WL; ++j) {
-      u32x4 v = ch.wv[j];
+      u32x4 v = ch.in ? ch.wv[j] : zero4;
       if constexpr (NORM) {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
@@ -191,7 +198,7 @@ __global__ __launch_bounds__(kLinThreads, lin_waves_per_eu(MT, SMALL, BNV)) void
 #pragma unroll
     for (int j = 0; j < AL; ++j) {
       const int m = rr + RPI * j;
-      *reinterpret_cast<u32x4*>(st + (WR + m) * STR + cc * 8) = m < M ? ch.xv[j] : zero4;
+      *reinterpret_cast<u32x4*>(st + (WR + m) * STR + cc * 8) = m < M && ch.in ? ch.xv[j] : zero4;
     }
     __builtin_amdgcn_wave_barrier();
     // operand reads: lane (g4, c) takes row c, elements 32 s + 8 g4 .. +7
@@ -212,14 +219,13 @@ __global__ __launch_bounds__(kLinThreads, lin_waves_per_eu(MT, SMALL, BNV)) void
     __builtin_amdgcn_wave_barrier();
   };
 
-  // ---- two-stage pipeline over this wave's chunks
-  Chunk A, B;
-  auto k_of = [&](int i) { return (worker + i * nworkers) * KC; };
-  if (nchunk > 0) issue(A, k_of(0));  // the first chunk streams in during the prologue below
-  // residual epilogue: this thread's 4 residual elements do not depend on the
-  // product, so their load is issued now rather than after the reduction
-  // (one memory round trip less at the end; the tile's columns are read and
-  // rewritten by this workgroup only)
+  // ---- loads, in the order they are consumed: the residual elements of the
+  // residual epilogue (they do not depend on the product: loaded now rather
+  // than after the reduction, one memory round trip less at the end; the
+  // tile's columns are read and rewritten by this workgroup only), the
+  // producer's partial sums of squares of the RMSNorm prologue, then the
+  // first two chunks of the two-stage pipeline, which stream in during the
+  // prologue.  A wait for a load then never waits for a later one.
   uint2 resid_pre = make_uint2(0u, 0u);
   if constexpr (EPI == 2) {
     constexpr int QPR = BNV / 4;
@@ -227,17 +233,33 @@ __global__ __launch_bounds__(kLinThreads, lin_waves_per_eu(MT, SMALL, BNV)) void
     if (tid < MP * QPR && m < M)
       resid_pre = *reinterpret_cast<const uint2*>(a.resid + (int64_t)(row0 + m) * a.N + (int64_t)tile * BNV + 4 * q);
   }
-
-  // ---- RMSNorm prologue: 1 / rms per row from the producer's partial sums,
+  // RMSNorm prologue: 1 / rms per row from the producer's partial sums,
   // added in a fixed order (thread part p sums slots p, p + P, ...; row m
   // then sums the P part sums in order)
+  constexpr int P = kLinThreads / MP;
+  float ssv[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  const int ssm = tid % MP, ssp = tid / MP;
+  const bool ss_on = NORM && ssp < P && ssm < M;
   if constexpr (NORM) {
-    constexpr int P = kLinThreads / MP;
-    const int m = tid % MP, p = tid / MP;
+    if (ss_on) {
+      const float* src = a.ss_in + row0 + ssm;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) ssv[u] = ssp + u * P < a.nss_in ? src[(int64_t)(ssp + u * P) * a.M] : 0.f;
+    }
+  }
+  Chunk A, B;
+  // chunk i of this wave (past its last chunk: elements outside the
+  // reduction, read and never multiplied)
+  auto k_of = [&](int i) { return (worker + i * nworkers) * KC; };
+  issue(A, k_of(0));
+  issue(B, k_of(1));
+  if constexpr (NORM) {
     float s = 0.f;
-    if (p < P && m < M) {
-      const float* src = a.ss_in + row0 + m;
-      for (int j0 = p; j0 < a.nss_in; j0 += 8 * P) {  // 8 loads in flight per round trip
+    if (ss_on) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) s += ssv[u];
+      const float* src = a.ss_in + row0 + ssm;
+      for (int j0 = ssp + 8 * P; j0 < a.nss_in; j0 += 8 * P) {  // more slots: 8 loads in flight per round trip
         float v[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) v[u] = j0 + u * P < a.nss_in ? src[(int64_t)(j0 + u * P) * a.M] : 0.f;
@@ -246,26 +268,45 @@ __global__ __launch_bounds__(kLinThreads, lin_waves_per_eu(MT, SMALL, BNV)) void
       }
     }
     ss_s[tid] = s;
-    __syncthreads();
+    lds_barrier();
     if (tid < MP) {
       float t = 0.f;
       for (int q = 0; q < P; ++q) t += ss_s[q * MP + tid];
       inv_s[tid] = rsqrtf(t / (float)K + a.eps);
     }
-    __syncthreads();
+    lds_barrier();
   }
 
-  for (int i = 0; i < nchunk; i += 2) {
-    if (i + 1 < nchunk) issue(B, k_of(i + 1));
+  // (a symmetric loop body that issues only chunks of this wave, no exit in
+  // its middle, and each issue kept after the multiply that frees its
+  // registers: the compiler then counts the loads in flight exactly, a
+  // multiply waits for its own chunk only, and nothing is left in flight
+  // past the last chunk; the last one to three chunks are peeled)
+  int i = 0;
+  for (; i + 3 < nchunk; i += 2) {
     compute(A);
-    if (i + 1 < nchunk) {
-      if (i + 2 < nchunk) issue(A, k_of(i + 2));
-      compute(B);
-    }
+    __builtin_amdgcn_sched_barrier(0);
+    issue(A, k_of(i + 2));
+    __builtin_amdgcn_sched_barrier(0);
+    compute(B);
+    __builtin_amdgcn_sched_barrier(0);
+    issue(B, k_of(i + 3));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if (i + 2 < nchunk) {
+    compute(A);
+    __builtin_amdgcn_sched_barrier(0);
+    issue(A, k_of(i + 2));
+    __builtin_amdgcn_sched_barrier(0);
+    compute(B);
+    compute(A);
+  } else {
+    if (i < nchunk) compute(A);
+    if (i + 1 < nchunk) compute(B);
   }
 
   // ---- sum the waves' partial products: lane (g4, c) holds C[16mt + 4g4 + i][c]
-  __syncthreads();  // every wave is done with its staged weights (red aliases them)
+  lds_barrier();  // every wave is done with its staged weights (red aliases them)
   float* red = reinterpret_cast<float*>(smem);  // [kLinWaves][MP][WR + 1]
 #pragma unroll
   for (int nt = 0; nt < NTL; ++nt)
@@ -273,7 +314,7 @@ __global__ __launch_bounds__(kLinThreads, lin_waves_per_eu(MT, SMALL, BNV)) void
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int i = 0; i < 4; ++i) red[(w * MP + mt * 16 + g4 * 4 + i) * (WR + 1) + nt * 16 + c] = acc[nt][mt][i];
-  __syncthreads();
+  lds_barrier();
   if (WR == kBN && a.ks > 1) {  // split reductions run on 16-column tiles only
     // ---- split-K: publish this workgroup's tile partial; the tile's last
     // workgroup to finish sums the ks partials in order (deterministic) and

@@ -56,14 +56,6 @@ __device__ __forceinline__ int counter_slot(int pair) { return ((pair & 255) << 
 #define NSV_MAX_STAGES 4  // deepest key-split pipeline
 #endif
 
-// Workgroup barrier that orders LDS accesses only: unlike __syncthreads() it
-// does not wait for the wave's outstanding global loads, so a load pipeline
-// issued before it stays in flight.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
 
 // Pipeline depth of the d-sliced bf16 kernel.  Its slices re-read the pair's
 // K through L1, whose fill rate bounds it, and deeper pipelines only add
