@@ -127,6 +127,15 @@ __device__ __forceinline__ float2 load8_agent(__amdgpu_buffer_rsrc_t r, unsigned
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
+// A row's position (int64; every position a plan accepts, -1 included, fits
+// 32 bits) read as the low word of the little-endian value.  A 64-bit load
+// whose upper half is dead lets the compiler reuse that register while the
+// load is in flight, and the reuse then waits for the load: a whole memory
+// round trip before the first K/V load is issued.
+__device__ __forceinline__ int load_pos(const int64_t* positions, int64_t row) {
+  return reinterpret_cast<const int32_t*>(positions)[2 * row];
+}
+
 // Keys of sequence b the kernels visit: never past the block table's width,
 // the bound the reference's chunk loop has (layers/attention.py:572).
 __device__ __forceinline__ int context_len(const VerifyArgs& a, int b) {
@@ -306,7 +315,7 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
       const bool ok = (m < a.Mv) && (t < qlen);
       const int row = ok ? q0 + t : 0;
       const int gg = ok ? g : 0;
-      qpos[mt] = (int)a.positions[row];
+      qpos[mt] = load_pos(a.positions, row);
       const bf16_t* qrow = (const bf16_t*)a.q + ((int64_t)row * a.H + hk * a.Gs + a.g0 + gg) * DH;
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) qB[mt][ks] = as_bf16x8(load16(qrow + ks * 32 + g4 * 8));
@@ -784,7 +793,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
       const int m = mt * 16 + c;
       const int g = m / a.QL, t = m - g * a.QL;
       const bool ok = (m < a.Mv) && (t < qlen);
-      qpos[mt] = (int)a.positions[ok ? q0 + t : 0];
+      qpos[mt] = load_pos(a.positions, ok ? q0 + t : 0);
     }
     // padded and missing rows read the sequence's first row (their scores are masked)
 #pragma unroll
@@ -1335,7 +1344,7 @@ __global__ __launch_bounds__(64) void verify_attn_f32_kernel(VerifyArgs a) {
     const int m = a.m_base + lane;
     const int g = m / a.QL, t = m - g * a.QL;
     const bool ok = (m < a.Mv) && (t < qlen);
-    pos_s[lane] = ok ? (int)a.positions[q0 + t] : -1;
+    pos_s[lane] = ok ? load_pos(a.positions, q0 + t) : -1;
   }
   __syncthreads();
 
