@@ -138,10 +138,15 @@ __device__ __forceinline__ int load_pos(const int64_t* positions, int64_t row) {
 
 // Keys of sequence b the kernels visit: never past the block table's width,
 // the bound the reference's chunk loop has (layers/attention.py:572).
+// (A workgroup's per-sequence values are read by every lane and made
+// wave-uniform: the compiler cannot prove on its own that memory the kernel
+// also writes holds the same value for every lane, and would keep them per
+// lane, each use as a scalar operand then a loop over the lanes' values.)
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 __device__ __forceinline__ int context_len(const VerifyArgs& a, int b) {
   const int64_t ctx = a.context_lens[b];
   const int64_t cap = (int64_t)a.max_blocks << a.bs_log2;
-  return (int)(ctx < 0 ? 0 : (ctx < cap ? ctx : cap));
+  return uniform((int)(ctx < 0 ? 0 : (ctx < cap ? ctx : cap)));
 }
 
 // Keys per split of a sequence with ctx keys: the caller's fixed split, or
@@ -292,8 +297,8 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
     pv[i] = j < npg ? btrow[j] : -1;
   }
   const int ctx = context_len(a, b);
-  const int q0 = a.cu_seqlens_q[b];
-  const int qlen = a.cu_seqlens_q[b + 1] - q0;
+  const int q0 = uniform(a.cu_seqlens_q[b]);
+  const int qlen = uniform(a.cu_seqlens_q[b + 1]) - q0;
   __builtin_amdgcn_sched_barrier(0);
   const int nsplit = num_splits(a, ctx);
   if (split >= nsplit || qlen < 0) return;  // uniform per workgroup
@@ -769,8 +774,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
     pv[i] = j < a.max_blocks ? btrow[j] : -1;
   }
   const int ctx = context_len(a, b);
-  const int q0 = a.cu_seqlens_q[b];
-  const int qlen = a.cu_seqlens_q[b + 1] - q0;
+  const int q0 = uniform(a.cu_seqlens_q[b]);
+  const int qlen = uniform(a.cu_seqlens_q[b + 1]) - q0;
   __builtin_amdgcn_sched_barrier(0);
   const int nsplit = num_splits(a, ctx);
   if (split >= nsplit || qlen < 0) return;  // uniform per workgroup
@@ -1187,7 +1192,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
     is_last = __hip_atomic_fetch_add(&a.counters[counter_slot(pair)], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
               (unsigned)(nsplit - 1);
   __syncthreads();
-  if (!is_last) return;
+  if (!uniform(is_last)) return;
   if (tid == 0) __hip_atomic_store(&a.counters[counter_slot(pair)], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int64_t base0 = (int64_t)pair * a.S * a.Mv;  // row 0 of split 0
   const __amdgpu_buffer_rsrc_t ors = block_rsrc(a.part_o + base0 * DH);   // the pair's partial rows
@@ -1211,7 +1216,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
     *dst = make_uint2(lo, hi);
   };
   // a real split other than this one (its values are loaded and not used)
-  auto other = [&](int sp) { return (sp < nsplit && sp != split) ? sp : (split == 0 ? 1 : 0); };
+  auto other = [&](int sp) { return uniform((sp < nsplit && sp != split) ? sp : (split == 0 ? 1 : 0)); };
   // Up to 8 splits: every value this thread merges, for all its items, in
   // one round trip (items past the rows load row 0 and are discarded).
   auto merge_in_one_trip = [&](auto width) {
@@ -1329,8 +1334,8 @@ __global__ __launch_bounds__(64) void verify_attn_f32_kernel(VerifyArgs a) {
   if (split >= nsplit) return;
   const int tok_begin = split * a.split_tokens;
   const int tok_end = min(ctx, tok_begin + a.split_tokens);
-  const int q0 = a.cu_seqlens_q[b];
-  const int qlen = a.cu_seqlens_q[b + 1] - q0;
+  const int q0 = uniform(a.cu_seqlens_q[b]);
+  const int qlen = uniform(a.cu_seqlens_q[b + 1]) - q0;
 
   // local row r serves query row m = m_base + r of the pair's Mv rows
   for (int idx = lane; idx < MP * DH; idx += NSV_WAVE) {
@@ -1464,8 +1469,8 @@ __global__ __launch_bounds__(256) void verify_merge_kernel(VerifyArgs a) {
   const int ctx = context_len(a, b);
   const int nsplit = num_splits(a, ctx);
   if (nsplit <= 1) return;  // written by the attention kernel itself
-  const int q0 = a.cu_seqlens_q[b];
-  const int qlen = a.cu_seqlens_q[b + 1] - q0;
+  const int q0 = uniform(a.cu_seqlens_q[b]);
+  const int qlen = uniform(a.cu_seqlens_q[b + 1]) - q0;
   const int g = m / a.QL, t = m - g * a.QL;
   if (t >= qlen) return;
   const int64_t base = (int64_t)pair * a.S * a.Mv + m;  // row of split 0
