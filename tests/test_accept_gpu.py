@@ -408,3 +408,51 @@ def test_accept_ratio_boundaries_multi_slab(dtype):
                                         temps[b], u[b], host(q)[b], dtype)
             assert len(want) == i + 1
             assert got[b] == want, (i, b, got[b], want)
+
+
+# Rows whose start is not 16-byte aligned (V odd: every other row of a bf16 batch, and V not a
+# multiple of 4 for fp32) take the element-by-element slab loads; V not a multiple of 8 leaves a
+# partial last group in every row.
+@pytest.mark.parametrize("dtype,V", [("bf16", 30001), ("f32", 30002), ("bf16", 1001)])
+def test_unaligned_rows(dtype, V):
+    print(f"case: unaligned rows {dtype} V={V}", flush=True)
+    B, K = 3, 4
+    # greedy
+    lg = logits_tensor(110, B * (K + 1), V, dtype)
+    am = lg.argmax(-1).tolist()
+    lists = [am[0:4], am[5:7] + [(am[7] + 1) % V], []]
+    d, nd = pad(lists, K)
+    got = results(*accept_greedy(lg, d, nd, K + 1))
+    assert got == oa.greedy_round(lists, host(lg), K + 1)
+    # stochastic, model drafts
+    dl, tl, lists = model_case(111, B, K, V, dtype)
+    u, q = draw_randomness([len(x) for x in lists], V, TDT[dtype], "cuda", True,
+                           torch.Generator(device="cuda").manual_seed(112))
+    d, nd = pad(lists, K)
+    got = results(*accept_stochastic(tl, d, nd, torch.tensor([1.0, 0.7, 1.0], device="cuda"), q, uniforms=u,
+                                     draft_logits=dl, target_seq_stride=K + 1, draft_seq_stride=K + 1,
+                                     draft_row_stride=1))
+    T, D, U, Q = host(tl), host(dl), u.cpu().numpy(), host(q)
+    for b, drafts in enumerate(lists):
+        k = len(drafts)
+        want = oa.verify_stochastic(drafts, T[b * (K + 1): b * (K + 1) + k + 1], D[b * (K + 1): b * (K + 1) + k],
+                                    [1.0, 0.7, 1.0][b], U[b, :k], Q[b], dtype)
+        assert got[b] == want, (b, got[b], want)
+    # stochastic, n-gram drafts (noise rows [K+1, V] per sequence, also unaligned)
+    am = tl.argmax(-1).tolist()
+    lists = [am[0:4], am[5:6], am[10:13]]
+    _, q = draw_randomness([len(x) for x in lists], V, TDT[dtype], "cuda", False,
+                           torch.Generator(device="cuda").manual_seed(113))
+    d, nd = pad(lists, K)
+    got = results(*accept_stochastic(tl, d, nd, torch.tensor([0.9, 1.0, 1.1], device="cuda"), q,
+                                     target_seq_stride=K + 1))
+    for b, drafts in enumerate(lists):
+        want = oa.verify(drafts, T[b * (K + 1): b * (K + 1) + len(drafts) + 1], None, [0.9, 1.0, 1.1][b], None,
+                         host(q)[b, :len(drafts) + 1], dtype)
+        assert got[b] == want, (b, got[b], want)
+    # the sampler over the same rows (fp32 noise [B, V])
+    rows = tl[:B]
+    temps = torch.tensor([1.0, 0.0, 0.6], device="cuda")
+    qn = torch.empty(B, V, device="cuda").exponential_(1, generator=torch.Generator(device="cuda").manual_seed(114))
+    qn.clamp_min_(1e-10)
+    assert sample(rows, temps, qn).tolist() == oa.sample_rows(host(rows), temps.cpu().numpy(), qn.cpu().numpy())
