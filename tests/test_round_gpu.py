@@ -113,16 +113,18 @@ def test_one_round_matches_host_restatement():
         assert int(r.committed[b]) == len(accepted[b])
 
 
-@pytest.mark.parametrize("block_size", [16, 64])
-def test_greedy_spec_equals_plain_decode_and_graph_equals_eager(block_size):
-    print(f"case: e2e spec==plain bs={block_size}", flush=True)
+# K = 40: 41 verify rows per sequence (two query heads per kv head: 82 rows, served one head at a
+# time by the attention), acceptance walks past lane 32
+@pytest.mark.parametrize("block_size,K", [(16, 6), (64, 6), (16, 40)])
+def test_greedy_spec_equals_plain_decode_and_graph_equals_eager(block_size, K):
+    print(f"case: e2e spec==plain bs={block_size} K={K}", flush=True)
     rng = np.random.default_rng(1)
     prompts = []
     for b in range(3):
         spans = [[int(x) for x in rng.integers(0, 2048, 10)] for _ in range(4)]
         prompts.append([t for i in range(12) for t in spans[i % 4]] + spans[0][:3])
     sp = SamplingParams(temperature=0.0, max_tokens=40, ignore_eos=True)
-    base = dict(model_config=TINY, num_speculative_tokens=6, ngram_min_size=2, ngram_max_size=4,
+    base = dict(model_config=TINY, num_speculative_tokens=K, ngram_min_size=2, ngram_max_size=4,
                 max_num_sequences=4, max_model_length=512, block_size=block_size, seed=3)
     out = {}
     for name, extra in [("spec", {}), ("plain", {"spec_method": "none"}), ("spec_eager", {"enforce_eager": True})]:
