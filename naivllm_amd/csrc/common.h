@@ -134,6 +134,28 @@ __device__ __forceinline__ void head_norm_rope(float x1, float x2, float inv, fl
   o2 = f32_to_bf16_bits(y1 * s + y2 * c);
 }
 
+// Stores / loads with the cache policy of agent-scope (device-coherent)
+// accesses (sc1: written through to, and read from, the device's point of
+// coherence), through a buffer resource whose wave-uniform base is the
+// caller's block: one instruction per 4 floats instead of two 64-bit
+// atomics.  Nothing needs them single-copy atomic where readers load only
+// after every writer's stores were acknowledged (the in-kernel merges).
+constexpr int kCpolSc1 = 16;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t block_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
+}
+// Offsets: a per-lane byte offset plus a wave-uniform one.
+__device__ __forceinline__ void store16_agent(__amdgpu_buffer_rsrc_t r, unsigned byte_off, f32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, (int)byte_off, 0, kCpolSc1);
+}
+__device__ __forceinline__ f32x4 load16_agent(__amdgpu_buffer_rsrc_t r, unsigned byte_off, unsigned uniform_off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, (int)uniform_off, kCpolSc1));
+}
+__device__ __forceinline__ float2 load8_agent(__amdgpu_buffer_rsrc_t r, unsigned byte_off, unsigned uniform_off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)byte_off, (int)uniform_off, kCpolSc1);
+  return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
+}
+
 // Workgroup barrier that orders LDS accesses only: unlike __syncthreads() it
 // does not wait for the wave's outstanding global loads, so a load pipeline
 // issued before it stays in flight.

@@ -43,6 +43,7 @@ constexpr int kMaxRows = 80;       // activation rows (5 MFMA row tiles)
 // atomics on one line serialise, ~20 ns apiece); tile t + 256 k shares
 // t's line.  Splitting needs fewer than 128 column tiles, well inside.
 constexpr int kMaxCounterTiles = 16384;
+constexpr int kMaxSplits = 4;      // workgroups a tile's reduction is split over, at most
 __device__ __forceinline__ int lin_counter_slot(int tile) { return ((tile & 255) << 6) | (tile >> 8); }
 
 struct LinearArgs {
@@ -315,32 +316,37 @@ __global__ __launch_bounds__(kLinThreads, lin_waves_per_eu(MT, SMALL, BNV)) void
 #pragma unroll
       for (int i = 0; i < 4; ++i) red[(w * MP + mt * 16 + g4 * 4 + i) * (WR + 1) + nt * 16 + c] = acc[nt][mt][i];
   lds_barrier();
-  if (WR == kBN && a.ks > 1) {  // split reductions run on 16-column tiles only
+  // split reductions run on 16-column tiles only; after one, red's wave-0
+  // slot holds the tile's total and the epilogue reads only that slot
+  bool split_total = false;
+  if (WR == kBN && a.ks > 1) {
     // ---- split-K: publish this workgroup's tile partial; the tile's last
-    // workgroup to finish sums the ks partials in order (deterministic) and
-    // runs the epilogue.  Ordering without release/acquire (which on gfx950
-    // would write back and invalidate whole L2s): every partial is written
-    // and read with agent-scope relaxed atomics (sc1: performed at the
-    // device's point of coherence, never served from a stale cached copy);
-    // each thread waits for its stores' acknowledgement (vmcnt(0)) before the
-    // barrier that precedes the arrival atomic, and the last workgroup issues
-    // its loads only after the counter's value came back.
+    // workgroup to finish sums the ks partials in split order (deterministic)
+    // and runs the epilogue.  Ordering without release/acquire (which on
+    // gfx950 would write back and invalidate whole L2s): every partial is
+    // written and read with the agent-scope cache policy (sc1: performed at
+    // the device's point of coherence, never served from a stale cached
+    // copy); each thread waits for its stores' acknowledgement (vmcnt(0))
+    // before the barrier that precedes the arrival atomic, and the last
+    // workgroup issues its loads only after the counter's value came back.
     const int m = tid >> 2, q = tid & 3;
-    float* pt = a.part + (int64_t)tile * a.ks * (kMaxRows * kBN);
-    if (tid < MP * 4 && m < M) {
-      float v[4];
+    const bool item = tid < MP * 4 && m < M;
+    f32x4 v = {0.f, 0.f, 0.f, 0.f};
+    if (item) {
+      float w8[kLinWaves][4];  // every wave's sums first (one LDS round trip), then the adds
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v[e] = 0.f;
+      for (int ww = 0; ww < kLinWaves; ++ww)
 #pragma unroll
-        for (int ww = 0; ww < kLinWaves; ++ww) v[e] += red[(ww * MP + m) * (kBN + 1) + 4 * q + e];
-      }
-      uint64_t* dst = reinterpret_cast<uint64_t*>(pt + (int64_t)kz * (kMaxRows * kBN) + m * kBN + 4 * q);
-      __hip_atomic_store(dst, (uint64_t)__float_as_uint(v[0]) | ((uint64_t)__float_as_uint(v[1]) << 32),
-                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(dst + 1, (uint64_t)__float_as_uint(v[2]) | ((uint64_t)__float_as_uint(v[3]) << 32),
-                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int e = 0; e < 4; ++e) w8[ww][e] = red[(ww * MP + m) * (kBN + 1) + 4 * q + e];
+#pragma unroll
+      for (int ww = 0; ww < kLinWaves; ++ww)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] += w8[ww][e];
     }
+    const __amdgpu_buffer_rsrc_t prs = block_rsrc(a.part + (int64_t)tile * a.ks * (kMaxRows * kBN));
+    const unsigned ioff = (unsigned)(m * kBN + 4 * q) * 4u;             // the item in one split's block
+    constexpr unsigned kSplitBytes = kMaxRows * kBN * 4u;                  // one split's block
+    if (item) store16_agent(prs, ioff + (unsigned)kz * kSplitBytes, v);
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     __shared__ int last;
@@ -348,34 +354,34 @@ __global__ __launch_bounds__(kLinThreads, lin_waves_per_eu(MT, SMALL, BNV)) void
       last = __hip_atomic_fetch_add(&a.counters[lin_counter_slot(tile)], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
              (unsigned)(a.ks - 1);
     __syncthreads();
-    if (!last) return;
+    if (!__builtin_amdgcn_readfirstlane(last)) return;
     if (tid == 0) __hip_atomic_store(&a.counters[lin_counter_slot(tile)], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // the tile's total into wave 0's slot of red, zeros in the others, so the
-    // epilogue below reads it unchanged
-    if (tid < MP * 4 && m < M) {
-      float v[4] = {0.f, 0.f, 0.f, 0.f};
-      for (int z = 0; z < a.ks; ++z) {
-        const uint64_t* src = reinterpret_cast<const uint64_t*>(pt + (int64_t)z * (kMaxRows * kBN) + m * kBN + 4 * q);
-        const uint64_t lo = __hip_atomic_load(const_cast<uint64_t*>(src), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const uint64_t hi = __hip_atomic_load(const_cast<uint64_t*>(src + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        v[0] += __uint_as_float((uint32_t)lo);
-        v[1] += __uint_as_float((uint32_t)(lo >> 32));
-        v[2] += __uint_as_float((uint32_t)hi);
-        v[3] += __uint_as_float((uint32_t)(hi >> 32));
-      }
+    // every other split's partial in one round trip (splits past ks and this
+    // workgroup's own read its own block and are not used), then the sum in
+    // split order, this workgroup's own partial from registers
+    f32x4 pz[kMaxSplits];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        red[m * (kBN + 1) + 4 * q + e] = v[e];
-#pragma unroll
-        for (int ww = 1; ww < kLinWaves; ++ww) red[(ww * MP + m) * (kBN + 1) + 4 * q + e] = 0.f;
-      }
+    for (int z = 0; z < kMaxSplits; ++z) {
+      const int zz = __builtin_amdgcn_readfirstlane(z < a.ks && z != kz ? z : kz);
+      pz[z] = load16_agent(prs, ioff, (unsigned)zz * kSplitBytes);
     }
-    __syncthreads();
+    f32x4 t = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int z = 0; z < kMaxSplits; ++z)
+      if (z < a.ks) t += z == kz ? v : pz[z];
+    if (item) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) red[m * (kBN + 1) + 4 * q + e] = t[e];
+    }
+    lds_barrier();
+    split_total = true;
   }
   auto colsum = [&](int m, int col) {
-    float v = 0.f;
+    float v = red[m * (WR + 1) + col];
+    if (!split_total) {
 #pragma unroll
-    for (int ww = 0; ww < kLinWaves; ++ww) v += red[(ww * MP + m) * (WR + 1) + col];
+      for (int ww = 1; ww < kLinWaves; ++ww) v += red[(ww * MP + m) * (WR + 1) + col];
+    }
     return NORM ? v * inv_s[m] : v;
   };
   if constexpr (EPI == 1) {
@@ -484,7 +490,7 @@ int linear_splits(int M, int N, int K) {
   const int tiles = N / kBN;
   if (M < 32 || M > kMaxRows || tiles >= 128) return 1;
   int ks = 256 / tiles;
-  ks = ks > 4 ? 4 : (ks < 1 ? 1 : ks);
+  ks = ks > kMaxSplits ? kMaxSplits : (ks < 1 ? 1 : ks);
   while (ks > 1 && K < ks * kLinWaves * 64) --ks;  // every worker keeps a chunk of the larger size
   return ks;
 }

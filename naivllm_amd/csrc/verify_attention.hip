@@ -104,26 +104,6 @@ __device__ __forceinline__ void store_agent(uint64_t* p, float x, float y) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// 16-byte stores / loads with the cache policy of the agent-scope accesses
-// above (sc1), through a buffer resource whose wave-uniform base is the
-// caller's block: one instruction per 4 floats instead of two 64-bit atomics.
-// Nothing needs them single-copy atomic: readers only load after every
-// writer's stores were acknowledged (see the merge below).
-constexpr int kCpolSc1 = 16;
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t block_rsrc(const void* base) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
-}
-// Offsets: a per-lane byte offset plus a wave-uniform one.
-__device__ __forceinline__ void store16_agent(__amdgpu_buffer_rsrc_t r, unsigned byte_off, f32x4 v) {
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, (int)byte_off, 0, kCpolSc1);
-}
-__device__ __forceinline__ f32x4 load16_agent(__amdgpu_buffer_rsrc_t r, unsigned byte_off, unsigned uniform_off) {
-  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)byte_off, (int)uniform_off, kCpolSc1));
-}
-__device__ __forceinline__ float2 load8_agent(__amdgpu_buffer_rsrc_t r, unsigned byte_off, unsigned uniform_off) {
-  const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)byte_off, (int)uniform_off, kCpolSc1);
-  return make_float2(__uint_as_float(v[0]), __uint_as_float(v[1]));
-}
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
