@@ -230,9 +230,8 @@ __global__ __launch_bounds__(kLinThreads, lin_waves_per_eu(MT, SMALL, BNV)) void
   uint2 resid_pre = make_uint2(0u, 0u);
   if constexpr (EPI == 2) {
     constexpr int QPR = BNV / 4;
-    const int m = tid / QPR, q = tid % QPR;
-    if (tid < MP * QPR && m < M)
-      resid_pre = *reinterpret_cast<const uint2*>(a.resid + (int64_t)(row0 + m) * a.N + (int64_t)tile * BNV + 4 * q);
+    const int m = min(tid / QPR, M - 1), q = tid % QPR;  // threads past the tile's rows load one and leave it unused
+    resid_pre = *reinterpret_cast<const uint2*>(a.resid + (int64_t)(row0 + m) * a.N + (int64_t)tile * BNV + 4 * q);
   }
   // RMSNorm prologue: 1 / rms per row from the producer's partial sums,
   // added in a fixed order (thread part p sums slots p, p + P, ...; row m
@@ -242,68 +241,88 @@ __global__ __launch_bounds__(kLinThreads, lin_waves_per_eu(MT, SMALL, BNV)) void
   const int ssm = tid % MP, ssp = tid / MP;
   const bool ss_on = NORM && ssp < P && ssm < M;
   if constexpr (NORM) {
-    if (ss_on) {
-      const float* src = a.ss_in + row0 + ssm;
+    // (unconditional loads, clamped to the last slot and row, zeros selected
+    // afterwards, in the prologue: a load under a branch, or a value used
+    // at once, is waited for on the spot)
+    const float* src = a.ss_in + row0 + min(ssm, M - 1);
 #pragma unroll
-      for (int u = 0; u < 8; ++u) ssv[u] = ssp + u * P < a.nss_in ? src[(int64_t)(ssp + u * P) * a.M] : 0.f;
-    }
+    for (int u = 0; u < 8; ++u) ssv[u] = src[(int64_t)min(ssp + u * P, a.nss_in - 1) * a.M];
   }
   Chunk A, B;
   // chunk i of this wave (past its last chunk: elements outside the
   // reduction, read and never multiplied)
   auto k_of = [&](int i) { return (worker + i * nworkers) * KC; };
-  issue(A, k_of(0));
-  issue(B, k_of(1));
-  if constexpr (NORM) {
-    float s = 0.f;
-    if (ss_on) {
+  auto prologue = [&]() {
+    if constexpr (NORM) {
+      // (the partial sums are taken here, after the chunks' loads were
+      // issued: the empty statement keeps the compiler from adding them up,
+      // and so waiting for them, ahead of those loads)
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int u = 0; u < 8; ++u) s += ssv[u];
-      const float* src = a.ss_in + row0 + ssm;
-      for (int j0 = ssp + 8 * P; j0 < a.nss_in; j0 += 8 * P) {  // more slots: 8 loads in flight per round trip
-        float v[8];
+      for (int u = 0; u < 8; ++u) __asm__ volatile("" : "+v"(ssv[u]) : : "memory");
+      float s = 0.f;
+      if (ss_on) {
 #pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = j0 + u * P < a.nss_in ? src[(int64_t)(j0 + u * P) * a.M] : 0.f;
+        for (int u = 0; u < 8; ++u) s += ssp + u * P < a.nss_in ? ssv[u] : 0.f;
+        const float* src = a.ss_in + row0 + ssm;
+        for (int j0 = ssp + 8 * P; j0 < a.nss_in; j0 += 8 * P) {  // more slots: 8 loads in flight per round trip
+          float v[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) s += v[u];
+          for (int u = 0; u < 8; ++u) v[u] = j0 + u * P < a.nss_in ? src[(int64_t)(j0 + u * P) * a.M] : 0.f;
+#pragma unroll
+          for (int u = 0; u < 8; ++u) s += v[u];
+        }
       }
+      ss_s[tid] = s;
+      lds_barrier();
+      if (tid < MP) {
+        float t = 0.f;
+        for (int q = 0; q < P; ++q) t += ss_s[q * MP + tid];
+        inv_s[tid] = rsqrtf(t / (float)K + a.eps);
+      }
+      lds_barrier();
     }
-    ss_s[tid] = s;
-    lds_barrier();
-    if (tid < MP) {
-      float t = 0.f;
-      for (int q = 0; q < P; ++q) t += ss_s[q * MP + tid];
-      inv_s[tid] = rsqrtf(t / (float)K + a.eps);
-    }
-    lds_barrier();
-  }
+  };
 
-  // (a symmetric loop body that issues only chunks of this wave, no exit in
-  // its middle, and each issue kept after the multiply that frees its
-  // registers: the compiler then counts the loads in flight exactly, a
-  // multiply waits for its own chunk only, and nothing is left in flight
-  // past the last chunk; the last one to three chunks are peeled)
-  int i = 0;
-  for (; i + 3 < nchunk; i += 2) {
-    compute(A);
-    __builtin_amdgcn_sched_barrier(0);
-    issue(A, k_of(i + 2));
-    __builtin_amdgcn_sched_barrier(0);
-    compute(B);
-    __builtin_amdgcn_sched_barrier(0);
-    issue(B, k_of(i + 3));
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  if (i + 2 < nchunk) {
-    compute(A);
-    __builtin_amdgcn_sched_barrier(0);
-    issue(A, k_of(i + 2));
-    __builtin_amdgcn_sched_barrier(0);
-    compute(B);
-    compute(A);
+  if (nchunk <= 1) {
+    // (one chunk or none, the common case of a short reduction: no second
+    // chunk's loads; the branch is uniform per wave, each side issues its
+    // loads unconditionally so the prologue waits for the partial sums only,
+    // and both run the prologue's barriers once)
+    issue(A, k_of(0));
+    prologue();
+    if (nchunk == 1) compute(A);
   } else {
-    if (i < nchunk) compute(A);
-    if (i + 1 < nchunk) compute(B);
+    issue(A, k_of(0));
+    issue(B, k_of(1));
+    prologue();
+    // (a symmetric loop body that issues only chunks of this wave, no exit in
+    // its middle, and each issue kept after the multiply that frees its
+    // registers: the compiler then counts the loads in flight exactly, a
+    // multiply waits for its own chunk only, and nothing is left in flight
+    // past the last chunk; the last two or three chunks are peeled)
+    int i = 0;
+    for (; i + 3 < nchunk; i += 2) {
+      compute(A);
+      __builtin_amdgcn_sched_barrier(0);
+      issue(A, k_of(i + 2));
+      __builtin_amdgcn_sched_barrier(0);
+      compute(B);
+      __builtin_amdgcn_sched_barrier(0);
+      issue(B, k_of(i + 3));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (i + 2 < nchunk) {
+      compute(A);
+      __builtin_amdgcn_sched_barrier(0);
+      issue(A, k_of(i + 2));
+      __builtin_amdgcn_sched_barrier(0);
+      compute(B);
+      compute(A);
+    } else {
+      compute(A);
+      compute(B);
+    }
   }
 
   // ---- sum the waves' partial products: lane (g4, c) holds C[16mt + 4g4 + i][c]
