@@ -1039,7 +1039,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
 #pragma unroll
     for (int ww = 0; ww < NW; ++ww) {
       rm[mt][ww] = red_m[ww][mt * 16 + c];
-      rl[mt][ww] = w == 0 ? red_l[ww][mt * 16 + c] : 0.f;
+      rl[mt][ww] = red_l[ww][mt * 16 + c];  // (used by wave 0; read by all: no branch per read)
     }
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -1199,13 +1199,17 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
   auto other = [&](int sp) { return uniform((sp < nsplit && sp != split) ? sp : (split == 0 ? 1 : 0)); };
   // Up to 8 splits: every value this thread merges, for all its items, in
   // one round trip (items past the rows load row 0 and are discarded).
+  // This split's own values are loaded too (they were acknowledged before
+  // the arrival), and splits past nsplit load split 0 and weigh 0: every
+  // loaded value is used on every path, so the compiler neither moves a load
+  // under a branch nor branches on which split is which.
   auto merge_in_one_trip = [&](auto width) {
     constexpr int CW = decltype(width)::value;
     float2 ml[MPASS][ITEMS][CW];
     f32x4 op[MPASS][ITEMS][CW];
 #pragma unroll
     for (int k = 0; k < CW; ++k) {
-      const unsigned rows = (unsigned)(other(k) * a.Mv);
+      const unsigned rows = (unsigned)(uniform(k < nsplit ? k : 0) * a.Mv);
 #pragma unroll
       for (int ps = 0; ps < MPASS; ++ps)
 #pragma unroll
@@ -1225,15 +1229,13 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
     for (int ps = 0; ps < MPASS; ++ps)
 #pragma unroll
       for (int j = 0; j < ITEMS; ++j) {
-        float ms[CW], ls[CW];
-        f32x4 os[CW];
+        float ms[CW];
         float M = kNegInf;
 #pragma unroll
         for (int k = 0; k < CW; ++k) {
-          const bool mine = k == split, used = k < nsplit;
-          ms[k] = !used ? kNegInf : (mine ? ims[ps][j] : ml[ps][j][k].x);
-          ls[k] = !used ? 0.f : (mine ? ils[ps][j] : ml[ps][j][k].y);
-          os[k] = !used ? f32x4{0.f, 0.f, 0.f, 0.f} : (mine ? own[ps][j] : op[ps][j][k]);
+          // (a split past nsplit: its max moved to -inf, so its weight is 0;
+          // every stored max is finite or -inf)
+          ms[k] = ml[ps][j][k].x + (k < nsplit ? 0.f : kNegInf);
           M = fmaxf(M, ms[k]);
         }
         const float ref = M == kNegInf ? 0.f : M;
@@ -1242,8 +1244,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
 #pragma unroll
         for (int k = 0; k < CW; ++k) {
           const float wk = __builtin_amdgcn_exp2f(ms[k] - ref);  // -inf: 0
-          den = fmaf(ls[k], wk, den);
-          num += os[k] * wk;
+          den = fmaf(ml[ps][j][k].y, wk, den);
+          num += op[ps][j][k] * wk;
         }
         dens[ps][j] = den;
         nums[ps][j] = num;
