@@ -123,11 +123,27 @@ __device__ __forceinline__ int load_pos(const int64_t* positions, int64_t row) {
 // also writes holds the same value for every lane, and would keep them per
 // lane, each use as a scalar operand then a loop over the lanes' values.)
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
-__device__ __forceinline__ int context_len(const VerifyArgs& a, int b) {
-  const int64_t ctx = a.context_lens[b];
+// The kernel arguments a kernel's first round trip needs, fetched in one
+// batch at its start: the empty statements use them, so the compiler cannot
+// defer one of their loads past the first use of another (each deferred load
+// is a dependent round trip of its own before the first K/V load).
+__device__ __forceinline__ void fetch_args(const VerifyArgs& a) {
+  __asm__ volatile("" ::"s"(a.block_tables), "s"(a.context_lens), "s"(a.cu_seqlens_q), "s"(a.P8), "s"(a.npairs),
+                   "s"(a.Hkv), "s"(a.max_blocks), "s"(a.bs_log2), "s"(a.split_tokens), "s"(a.dqc), "s"(a.ks_splits),
+                   "s"(a.S), "s"(a.Mv), "s"(a.QL));
+}
+// The sequence's context length and query range, used here so that their
+// loads stay ahead of every exit (a load whose value only a later block uses
+// is otherwise moved into that block, behind the exit's branch).
+__device__ __forceinline__ void pin_metadata(int64_t ctx, int q0, int q1) {
+  __asm__ volatile("" ::"s"(ctx), "s"(q0), "s"(q1));
+}
+
+__device__ __forceinline__ int clamp_context(const VerifyArgs& a, int64_t ctx) {
   const int64_t cap = (int64_t)a.max_blocks << a.bs_log2;
   return uniform((int)(ctx < 0 ? 0 : (ctx < cap ? ctx : cap)));
 }
+__device__ __forceinline__ int context_len(const VerifyArgs& a, int b) { return clamp_context(a, a.context_lens[b]); }
 
 // Keys per split of a sequence with ctx keys: the caller's fixed split, or
 // (key-split kernel, automatic) ctx spread evenly over ks_splits splits in
@@ -251,10 +267,15 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
   // ---- workgroup -> (pair, dq, split); every workgroup of a pair on one XCD
   const int wg = blockIdx.x;
   const int yy = wg >> 3;
-  const int pair = (yy % a.P8) * 8 + (wg & 7);
+  fetch_args(a);
+  const int pair_raw = (yy % a.P8) * 8 + (wg & 7);
   const int rest = yy / a.P8;
   const int dq = rest % a.dqc, split = rest / a.dqc;
-  if (pair >= a.npairs) return;  // grid rounds the pair count up to a multiple of 8
+  // (the grid rounds the pair count up to a multiple of 8: workgroups past
+  // the last pair, or past the table's keys, read clamped metadata and leave
+  // once it is back -- an exit before those loads would put the kernel
+  // arguments the loads need into a second, dependent round trip)
+  const int pair = min(pair_raw, a.npairs - 1);
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g4 = lane >> 4, c = lane & 15;
@@ -262,24 +283,24 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
   const int max_ctx = a.max_blocks << a.bs_log2;
   const int tok_begin = split * a.split_tokens;
   const int range_end = min(max_ctx, tok_begin + a.split_tokens);
-  if (tok_begin >= max_ctx) return;
 
   // ---- first round trip: the split's block-table slice, context length and
-  // query-row range, all independent
+  // query-row range, all independent and issued before any is used
+  // (entries past the slice read the row's last one and are not stored)
   const int pg0 = tok_begin >> a.bs_log2;
   const int npg = ((range_end - 1) >> a.bs_log2) - pg0 + 1;
-  const int32_t* btrow = a.block_tables + (int64_t)b * a.max_blocks + pg0;
+  const int32_t* btrow = a.block_tables + (int64_t)b * a.max_blocks;
   constexpr int PPT = (kMaxSplitPages + NT - 1) / NT;
   int pv[PPT];
 #pragma unroll
-  for (int i = 0; i < PPT; ++i) {
-    const int j = tid + i * NT;
-    pv[i] = j < npg ? btrow[j] : -1;
-  }
-  const int ctx = context_len(a, b);
+  for (int i = 0; i < PPT; ++i) pv[i] = btrow[min(pg0 + tid + i * NT, a.max_blocks - 1)];
+  const int64_t ctx_raw = a.context_lens[b];
   const int q0 = uniform(a.cu_seqlens_q[b]);
-  const int qlen = uniform(a.cu_seqlens_q[b + 1]) - q0;
-  __builtin_amdgcn_sched_barrier(0);
+  const int q1 = uniform(a.cu_seqlens_q[b + 1]);
+  pin_metadata(ctx_raw, q0, q1);
+  if (pair_raw >= a.npairs || tok_begin >= max_ctx) return;
+  const int ctx = clamp_context(a, ctx_raw);
+  const int qlen = q1 - q0;
   const int nsplit = num_splits(a, ctx);
   if (split >= nsplit || qlen < 0) return;  // uniform per workgroup
   const int tok_end = min(ctx, range_end);
@@ -736,27 +757,34 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
   // ---- workgroup -> (pair, split); every split of a pair on one XCD
   const int wg = blockIdx.x;
   const int yy = wg >> 3;
-  const int pair = (yy % a.P8) * 8 + (wg & 7);
+  fetch_args(a);
+  const int pair_raw = (yy % a.P8) * 8 + (wg & 7);
   const int split = yy / a.P8;
-  if (pair >= a.npairs) return;  // grid rounds the pair count up to a multiple of 8
+  // (the grid rounds the pair count up to a multiple of 8: workgroups past
+  // the last pair read its metadata and leave once it is back -- an exit
+  // before those loads would put the kernel arguments the loads need into a
+  // second, dependent round trip)
+  const int pair = min(pair_raw, a.npairs - 1);
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g4 = lane >> 4, c = lane & 15;
   const int b = pair / a.Hkv, hk = pair - b * a.Hkv;
 
-  // ---- first round trip: block-table row, context length, query range
+  // ---- first round trip: block-table row, context length, query range, all
+  // issued before any is used (entries past the row read its last one and
+  // are not stored)
   const int32_t* btrow = a.block_tables + (int64_t)b * a.max_blocks;
   constexpr int PPT = (kMaxSplitPages + NT - 1) / NT;
   int pv[PPT];
 #pragma unroll
-  for (int i = 0; i < PPT; ++i) {
-    const int j = tid + i * NT;
-    pv[i] = j < a.max_blocks ? btrow[j] : -1;
-  }
-  const int ctx = context_len(a, b);
+  for (int i = 0; i < PPT; ++i) pv[i] = btrow[min(tid + i * NT, a.max_blocks - 1)];
+  const int64_t ctx_raw = a.context_lens[b];
   const int q0 = uniform(a.cu_seqlens_q[b]);
-  const int qlen = uniform(a.cu_seqlens_q[b + 1]) - q0;
-  __builtin_amdgcn_sched_barrier(0);
+  const int q1 = uniform(a.cu_seqlens_q[b + 1]);
+  pin_metadata(ctx_raw, q0, q1);
+  if (pair_raw >= a.npairs) return;
+  const int ctx = clamp_context(a, ctx_raw);
+  const int qlen = q1 - q0;
   const int nsplit = num_splits(a, ctx);
   if (split >= nsplit || qlen < 0) return;  // uniform per workgroup
   const int len = split_len(a, ctx);
@@ -1443,19 +1471,39 @@ template <typename OutT, int E>
 __global__ __launch_bounds__(256) void verify_merge_kernel(VerifyArgs a) {
   constexpr int DH = 64 * E;
   constexpr int CH = 8;  // splits per round trip
-  const int pair = blockIdx.x;
-  const int m = blockIdx.y * 4 + (threadIdx.x >> 6);
+  fetch_args(a);
+  const int pair = min((int)blockIdx.x, a.npairs - 1);
+  const int m_raw = blockIdx.y * 4 + (threadIdx.x >> 6);
+  const int m = min(m_raw, a.Mv - 1);
   const int lane = threadIdx.x & 63;
-  if (pair >= a.npairs || m >= a.Mv) return;
   const int b = pair / a.Hkv, hk = pair - b * a.Hkv;
-  const int ctx = context_len(a, b);
+  const int64_t base = (int64_t)pair * a.S * a.Mv + m;  // row of split 0
+  // The first CH splits' values are loaded with the metadata, in one round
+  // trip (exits only after every load was issued; splits past the plan's S
+  // read split 0).  Splits the sequence does not have hold stale values,
+  // possibly not finite: they are masked off bitwise, not multiplied by a
+  // zero weight.
+  float2 ml0[CH];
+  float os0[CH][E];
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    const int64_t r = base + (int64_t)(j < a.S ? j : 0) * a.Mv;
+    ml0[j] = *reinterpret_cast<const float2*>(&a.part_ml[r * 2]);
+#pragma unroll
+    for (int e = 0; e < E; ++e) os0[j][e] = a.part_o[r * DH + e * 64 + lane];
+  }
+  const int64_t ctx_raw = a.context_lens[b];
+  const int q0 = uniform(a.cu_seqlens_q[b]);
+  const int q1 = uniform(a.cu_seqlens_q[b + 1]);
+  pin_metadata(ctx_raw, q0, q1);
+  if ((int)blockIdx.x >= a.npairs || m_raw >= a.Mv) return;
+  const int ctx = clamp_context(a, ctx_raw);
   const int nsplit = num_splits(a, ctx);
   if (nsplit <= 1) return;  // written by the attention kernel itself
-  const int q0 = uniform(a.cu_seqlens_q[b]);
-  const int qlen = uniform(a.cu_seqlens_q[b + 1]) - q0;
+  const int qlen = q1 - q0;
   const int g = m / a.QL, t = m - g * a.QL;
   if (t >= qlen) return;
-  const int64_t base = (int64_t)pair * a.S * a.Mv + m;  // row of split 0
+  auto keep = [](float v, uint32_t mask, uint32_t other) { return __uint_as_float((__float_as_uint(v) & mask) | (other & ~mask)); };
   float M = kNegInf, den = 0.f, num[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) num[e] = 0.f;
@@ -1463,13 +1511,24 @@ __global__ __launch_bounds__(256) void verify_merge_kernel(VerifyArgs a) {
     float ms[CH], ls[CH], os[CH][E];
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
-      const int sp = s0 + j < nsplit ? s0 + j : s0;
-      const int64_t r = base + (int64_t)sp * a.Mv;
-      const float2 ml = *reinterpret_cast<const float2*>(&a.part_ml[r * 2]);
-      ms[j] = s0 + j < nsplit ? ml.x : kNegInf;
-      ls[j] = ml.y;
+      float2 ml;
+      float o[E];
+      if (s0 == 0) {
+        ml = ml0[j];
 #pragma unroll
-      for (int e = 0; e < E; ++e) os[j][e] = a.part_o[r * DH + e * 64 + lane];
+        for (int e = 0; e < E; ++e) o[e] = os0[j][e];
+      } else {
+        const int sp = s0 + j < nsplit ? s0 + j : s0;
+        const int64_t r = base + (int64_t)sp * a.Mv;
+        ml = *reinterpret_cast<const float2*>(&a.part_ml[r * 2]);
+#pragma unroll
+        for (int e = 0; e < E; ++e) o[e] = a.part_o[r * DH + e * 64 + lane];
+      }
+      const uint32_t mask = s0 + j < nsplit ? 0xffffffffu : 0u;  // absent split: max -inf, sum 0, values 0
+      ms[j] = keep(ml.x, mask, 0xff800000u);
+      ls[j] = keep(ml.y, mask, 0u);
+#pragma unroll
+      for (int e = 0; e < E; ++e) os[j][e] = keep(o[e], mask, 0u);
     }
     float Mn = M;
 #pragma unroll
