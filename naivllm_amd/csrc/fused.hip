@@ -131,35 +131,54 @@ struct EpilogueArgs {
   float eps;
 };
 
+// Every load of a wave is issued at its start, in one round trip: the row's
+// q/k/v head, its slot, the norm weight and (per-row table, POS false) the
+// rotary row; with positions (POS true) the rotary row waits for the
+// position.  Loads are unconditional (lanes past D/2 and waves past the last
+// head read clamped elements and leave): a load under a branch is waited for
+// on the spot.
+template <bool POS>
 __global__ __launch_bounds__(256) void qk_norm_rope_store_kernel(EpilogueArgs a) {
-  const int wave = (blockIdx.x * blockDim.x + threadIdx.x) >> 6;
-  const int lane = threadIdx.x & 63;
+  __asm__ volatile("" ::"s"(a.qkv), "s"(a.q_w), "s"(a.k_w), "s"(a.cos_sin), "s"(a.positions), "s"(a.slots),
+                   "s"(a.q_out), "s"(a.k_cache), "s"(a.v_cache), "s"(a.T), "s"(a.H), "s"(a.Hkv), "s"(a.D),
+                   "s"(a.max_pos), "s"(a.eps));
   const int heads = a.H + 2 * a.Hkv;
-  if (wave >= a.T * heads) return;
+  const int wave_raw = (blockIdx.x * 256 + threadIdx.x) >> 6;  // 256 threads: the launch's block size
+  const int wave = __builtin_amdgcn_readfirstlane(min(wave_raw, a.T * heads - 1));
+  const int lane = threadIdx.x & 63;
   const int row = wave / heads, head = wave - row * heads;
   const int half = a.D >> 1;
   const bool on = lane < half;
+  const int l = on ? lane : half - 1;
+  const bool is_q = head < a.H, is_v = head >= a.H + a.Hkv;
   const uint16_t* src = a.qkv + ((int64_t)row * heads + head) * a.D;
-  float x1 = on ? bf(src[lane]) : 0.f;
-  float x2 = on ? bf(src[lane + half]) : 0.f;
+  const uint16_t* w = is_q ? a.q_w : a.k_w;
+  const uint16_t s1 = src[l], s2 = src[l + half];
   const int64_t slot = a.slots[row];
-  if (head >= a.H + a.Hkv) {  // v head: store as is
+  const uint16_t w1 = w[l], w2 = w[l + half];
+  int64_t pos = row;
+  if constexpr (POS) {
+    pos = a.positions[row];
+    pos = pos < 0 ? 0 : (pos >= a.max_pos ? a.max_pos - 1 : pos);
+  }
+  const float c = a.cos_sin[pos * a.D + l], sn = a.cos_sin[pos * a.D + half + l];
+  // (used here, so that no load is moved behind the branches below, which
+  // only some heads take)
+  __asm__ volatile("" ::"v"(s1), "v"(s2), "v"(w1), "v"(w2), "v"(c), "v"(sn));
+  if (wave_raw >= a.T * heads) return;
+  if (is_v) {  // v head: store as is
     if (on && slot >= 0) {
       uint16_t* dst = a.v_cache + (slot * a.Hkv + (head - a.H - a.Hkv)) * a.D;
-      dst[lane] = src[lane];
-      dst[lane + half] = src[lane + half];
+      dst[lane] = s1;
+      dst[lane + half] = s2;
     }
     return;
   }
-  const bool is_q = head < a.H;
+  const float x1 = on ? bf(s1) : 0.f, x2 = on ? bf(s2) : 0.f;
   const float inv = head_inv_rms(wave_sum(head_sq(x1, x2)), a.D, a.eps);
-  const uint16_t* w = is_q ? a.q_w : a.k_w;
   if (on) {
-    int64_t pos = a.positions ? a.positions[row] : row;
-    pos = pos < 0 ? 0 : (pos >= a.max_pos ? a.max_pos - 1 : pos);
-    const float c = a.cos_sin[pos * a.D + lane], s = a.cos_sin[pos * a.D + half + lane];
     uint16_t o1, o2;
-    head_norm_rope(x1, x2, inv, bf(w[lane]), bf(w[lane + half]), c, s, o1, o2);
+    head_norm_rope(x1, x2, inv, bf(w1), bf(w2), c, sn, o1, o2);
     if (is_q) {
       uint16_t* dst = a.q_out + ((int64_t)row * a.H + head) * a.D;
       dst[lane] = o1;
@@ -225,8 +244,12 @@ int nsv_qk_norm_rope_store(const void* qkv, const void* q_norm_w, const void* k_
   EpilogueArgs a{(const uint16_t*)qkv, (const uint16_t*)q_norm_w, (const uint16_t*)k_norm_w, cos_sin, positions,
                  slot_mapping, (uint16_t*)q_out, (uint16_t*)k_cache, (uint16_t*)v_cache, T, H, Hkv, D, max_pos, eps};
   const int64_t waves = (int64_t)T * (H + 2 * Hkv);
-  hipLaunchKernelGGL(qk_norm_rope_store_kernel, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, (hipStream_t)stream,
-                     a);
+  if (positions)
+    hipLaunchKernelGGL(qk_norm_rope_store_kernel<true>, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
+                       (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(qk_norm_rope_store_kernel<false>, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0,
+                       (hipStream_t)stream, a);
   return nsv_launch_status();
 }
 
