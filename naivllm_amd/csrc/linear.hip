@@ -65,6 +65,7 @@ struct LinearArgs {
 __device__ __forceinline__ bf16x8 to_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 typedef float f32x2v __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
 // two floats to packed bf16, round to nearest even (gfx950's v_cvt_pk_bf16_f32)
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2v){lo, hi}, bf16x2v));
@@ -585,6 +586,162 @@ int launch_linear(const LinearArgs& a, const LinPlan& p, bool norm, int epi, hip
                  : launch_linear_tiles<MT, kBN, false>(a, norm, epi, grid, s);
 }
 
+
+// ---------------------------------------------------------------------------
+// Streaming projection for very wide outputs (the LM head: a vocabulary of
+// 151,936 weight rows): y[M, N] = x[M, K] W[N, K]^T with the plain epilogue,
+// for as many rows as the activations fit the LDS (M (K + 8) bf16).  One
+// workgroup per CU, its activations staged in LDS once; each wave then
+// streams whole 16-row weight tiles (tiles gw, gw + W, ... for global wave
+// gw of W), every 256-element group of a tile's rows loaded straight into
+// the MFMA A-operand layout (lane (g4, c): row c, 8 elements at 32 s + 8 g4)
+// while the previous group is multiplied, so each wave keeps two groups (16
+// KiB) in flight with no workgroup barrier after the staging and no
+// cross-wave reduction: a wave owns a tile's whole reduction.
+// ---------------------------------------------------------------------------
+constexpr int kStreamWaves = 8;
+constexpr int kStreamKG = 256;                 // reduction elements per load group: 8 MFMA k-steps
+constexpr int kStreamLds = 160 * 1024;         // LDS bytes a workgroup may hold (gfx950)
+
+struct StreamArgs {
+  const uint16_t* x;  // [M, K]
+  const uint16_t* w;  // [N, K]
+  uint16_t* y;        // [M, N]
+  int M, N, K;
+  int tiles;          // N / 16
+};
+
+template <int MT, int NG>  // NG = K / 256 load groups per tile
+__global__ __launch_bounds__(kStreamWaves * 64, 1) void stream_linear_kernel(StreamArgs a) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char xs_raw[];  // [M][K + 8] bf16
+  __asm__ volatile("" ::"s"(a.x), "s"(a.w), "s"(a.y), "s"(a.M), "s"(a.N), "s"(a.K), "s"(a.tiles));
+  constexpr int K = NG * kStreamKG;
+  constexpr int XSTR = K + 8;  // staged row stride (elements): the 16 rows of a B-operand read fall in distinct banks
+  uint16_t* xs = reinterpret_cast<uint16_t*>(xs_raw);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g4 = lane >> 4, c = lane & 15;
+  const int M = a.M;
+  const int nwaves = gridDim.x * kStreamWaves;
+  const int gw = blockIdx.x * kStreamWaves + w;
+  const int my_tiles = gw < a.tiles ? (a.tiles - gw + nwaves - 1) / nwaves : 0;  // uniform
+
+  // the activations, 16-byte chunks tid, tid + 512, ..., 8 loads per batch
+  const int chunks = M * (K / 8);
+  for (int i0 = 0; i0 < chunks; i0 += 8 * kStreamWaves * 64) {
+    u32x4 v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = min(i0 + j * kStreamWaves * 64 + tid, chunks - 1);
+      v[j] = *reinterpret_cast<const u32x4*>(a.x + (int64_t)i * 8);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = i0 + j * kStreamWaves * 64 + tid;
+      if (i < chunks) {
+        const int m = i / (K / 8), k8 = i - m * (K / 8);
+        *reinterpret_cast<u32x4*>(xs + m * XSTR + k8 * 8) = v[j];
+      }
+    }
+  }
+  __syncthreads();
+  if (my_tiles == 0) return;
+
+  // weight rows of this wave's tile i (past its last tile: the last again, read and never multiplied)
+  auto wrow = [&](int i) { return a.w + ((int64_t)(gw + min(i, my_tiles - 1) * nwaves) * 16 + c) * K + 8 * g4; };
+  auto issue = [&](u32x4 (&buf)[8], const uint16_t* p) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) buf[s] = *reinterpret_cast<const u32x4*>(p + 32 * s);
+  };
+  f32x4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  int brow[MT];  // staged row of each m-tile's B operand (rows past M read row M - 1; never stored)
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) brow[mt] = min(mt * 16 + c, M - 1) * XSTR + 8 * g4;
+  auto compute = [&](const u32x4 (&buf)[8], int kg) {
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const u32x4 bv = *reinterpret_cast<const u32x4*>(xs + brow[mt] + kg * kStreamKG + 32 * s);
+        acc[mt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(to_bf16x8(buf[s]), to_bf16x8(bv), acc[mt], 0, 0, 0);
+      }
+    }
+  };
+  // y through a buffer resource of exactly M rows: the stores of rows past M
+  // fall outside it and are dropped, so every store is unconditional (a
+  // store under a branch leaves the compiler's wait counts inexact)
+  const __amdgpu_buffer_rsrc_t yr =
+      __builtin_amdgcn_make_buffer_rsrc(a.y, (short)0, (int)((int64_t)M * a.N * 2), 0x00020000);
+  u32x4 A[8], B[8];
+  issue(A, wrow(0));
+  for (int i = 0; i < my_tiles; ++i) {
+    const uint16_t* p = wrow(i);
+    const uint16_t* pn = wrow(i + 1);
+    // (scheduling barriers keep each group's 8 loads together and after the
+    // multiplies that free their registers: the compiler otherwise spreads
+    // them between the multiplies, reusing registers of loads in flight)
+#pragma unroll
+    for (int kg = 0; kg < NG; kg += 2) {
+      __builtin_amdgcn_sched_barrier(0);
+      issue(B, p + (kg + 1) * kStreamKG);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(A, kg);
+      __builtin_amdgcn_sched_barrier(0);
+      issue(A, kg + 2 < NG ? p + (kg + 2) * kStreamKG : pn);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(B, kg + 1);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // lane (g4, c) holds y[16 mt + c][16 t + 4 g4 .. + 3]
+    const int t = gw + i * nwaves;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = mt * 16 + c;
+      const uint32_t lo = pack_bf16x2(acc[mt][0], acc[mt][1]), hi = pack_bf16x2(acc[mt][2], acc[mt][3]);
+      const unsigned off = (unsigned)(((int64_t)m * a.N + t * 16 + 4 * g4) * 2);
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2v, make_uint2(lo, hi)), yr, (int)off, 0, 0);
+      acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last (unused) group's loads
+}
+
+// Streaming kernel for a wide plain projection: at least four 16-row weight
+// tiles per wave (8 waves per CU), a reduction of 1024, 2048 or 4096
+// elements, and activations that fit the LDS.
+bool stream_wide(int M, int N, int K, bool norm, int epi, int cus) {
+  return !norm && epi == 0 && M >= 1 && M <= kMaxRows && (K == 1024 || K == 2048 || K == 4096) &&
+         (int64_t)(N / kBN) >= 32LL * cus && (int64_t)M * (K + 8) * 2 <= kStreamLds &&
+         (int64_t)M * N * 2 < ((int64_t)1 << 31);
+}
+
+template <int MT, int NG>
+int launch_stream(const StreamArgs& a, int cus, hipStream_t s) {
+  static int attr[64] = {0};  // per device: the dynamic LDS limit raised once
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return NSV_ERR_UNSUPPORTED;
+  if (!attr[dev]) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&stream_linear_kernel<MT, NG>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kStreamLds) != hipSuccess)
+      return nsv_launch_status();
+    attr[dev] = 1;
+  }
+  const size_t lds = (size_t)a.M * (a.K + 8) * 2;
+  hipLaunchKernelGGL((stream_linear_kernel<MT, NG>), dim3(cus), dim3(kStreamWaves * 64), lds, s, a);
+  return nsv_launch_status();
+}
+
+template <int MT>
+int launch_stream_k(const StreamArgs& a, int cus, hipStream_t s) {
+  switch (a.K) {
+    case 1024: return launch_stream<MT, 4>(a, cus, s);
+    case 2048: return launch_stream<MT, 8>(a, cus, s);
+    default: return launch_stream<MT, 16>(a, cus, s);  // 4096 (stream_wide admits no other)
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -619,6 +776,18 @@ int nsv_linear(const void* x, const void* norm_w, const float* ss_in, int nss_in
   if (norm_w && (!ss_in || nss_in <= 0)) return NSV_ERR_ARG;
   if (epilogue == 2 ? (!resid || !ss_out) : !y) return NSV_ERR_ARG;
   const bool norm = norm_w != nullptr;
+  if (stream_wide(M, N, K, norm, epilogue, lin_device_cus())) {
+    const StreamArgs sa{(const uint16_t*)x, (const uint16_t*)weight, (uint16_t*)y, M, N, K, N / kBN};
+    const int cus = lin_device_cus();
+    hipStream_t st = (hipStream_t)stream;
+    switch ((M + 15) / 16) {
+      case 1: return launch_stream_k<1>(sa, cus, st);
+      case 2: return launch_stream_k<2>(sa, cus, st);
+      case 3: return launch_stream_k<3>(sa, cus, st);
+      case 4: return launch_stream_k<4>(sa, cus, st);
+      default: return launch_stream_k<5>(sa, cus, st);
+    }
+  }
   const LinPlan p = linear_plan(M, N, K, norm, epilogue, lin_device_cus());
   const size_t need = linear_ws_bytes(p.ks, N);
   if (need && (!workspace || workspace_bytes < need)) return NSV_ERR_WORKSPACE;

@@ -153,9 +153,17 @@ FUSED_ROWS = 80
 FUSED_ROWS_WIDE = 12  # hidden size above 2048
 
 
-# Rows up to which the LM head runs on the few-row kernel (measured on
-# MI355X, the 0.6B head alone: 51.7 vs 55.6 us at 9 rows, 152 vs 86 us at 72).
-LM_HEAD_ROWS = 16
+# Rows up to which the LM head runs on this library's kernels: nsv_linear
+# streams a vocabulary-wide head's weight tiles while the activations fit its
+# LDS (rows x (hidden + 8) bf16 within 160 KiB), hipBLASLt's large tiles
+# beyond.  Measured on MI355X, graph-replayed, the 0.6B head alone: 58.6 vs
+# 58.6 us at 9 rows, 59.9 vs 69.2 at 18, 70.5 vs 83.7 at 72; the 8B head
+# (hidden 4096): 232 vs 248 us at 9 rows.
+LM_HEAD_LDS = 160 * 1024
+
+
+def lm_head_rows(hidden: int) -> int:
+    return max(16, min(79, LM_HEAD_LDS // ((hidden + 8) * 2)))
 
 
 def prefill_metadata(token_lists, starts, tables, block_size: int, q_block: int, device):
@@ -323,9 +331,10 @@ class Qwen3Verify:
         if logits_rows is not None:
             h = h.index_select(0, logits_rows)
             T = h.shape[0]
-        # the LM head: the few-row kernel up to LM_HEAD_ROWS rows (it streams the
-        # vocabulary's weight rows faster there), hipBLASLt's large tiles beyond
-        if T <= LM_HEAD_ROWS:
+        # the LM head: this library's streaming kernel up to lm_head_rows rows
+        # (it streams the vocabulary's weight rows faster there), hipBLASLt's
+        # large tiles beyond
+        if T <= lm_head_rows(E):
             if logits_out is None:
                 logits_out = torch.empty(T, self.lm_head.shape[0], dtype=self.dtype, device=self.device)
             linear(h, self.lm_head, logits_out)

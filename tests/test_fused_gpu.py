@@ -193,7 +193,7 @@ def test_forward_matches_dense_fp32(fused, bs, head_few, monkeypatch):
     print(f"case: qwen3 verify forward vs dense fp32, fused={fused} block_size={bs} head_few={head_few}", flush=True)
     monkeypatch.setattr(qm, "FUSED_ROWS", 1 << 30 if fused else 0)
     monkeypatch.setattr(qm, "FUSED_ROWS_WIDE", 1 << 30 if fused else 0)
-    monkeypatch.setattr(qm, "LM_HEAD_ROWS", 1 << 30 if head_few else 0)
+    monkeypatch.setattr(qm, "lm_head_rows", (lambda hidden: 1 << 30) if head_few else (lambda hidden: 0))
     cfg = Qwen3Config(vocab_size=2048, hidden_size=256, num_layers=2, num_heads=4, num_kv_heads=2, head_dim=64,
                       intermediate_size=512, max_position=4096)
     model = Qwen3Verify(cfg, "cuda", seed=3)

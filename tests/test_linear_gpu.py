@@ -187,3 +187,23 @@ def test_split_reduction_is_deterministic_and_reusable(M, N, K):
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
     prod = (x.float() @ w.float().t()).to(torch.bfloat16)
     torch.testing.assert_close(outs[0][0].float(), (prod.float() + r0.float()).to(torch.bfloat16).float(), **BF16)
+
+
+# The streaming kernel nsv_linear takes for very wide plain projections (the
+# LM head: at least 32 16-row tiles per CU), at the rows a verify round asks
+# logits for (b1, b2, b8), the 8B head's reduction, and the row count past its
+# LDS capacity at K = 1024 (80 rows: the 16-column kernel again).
+WIDE = [(9, 151936, 1024), (1, 151936, 1024), (18, 151936, 1024), (72, 151936, 1024), (80, 151936, 1024),
+        (9, 151936, 4096), (16, 135168, 2048)]
+
+
+@pytest.mark.parametrize("M,N,K", WIDE)
+def test_linear_wide(M, N, K):
+    print(f"case: linear wide M={M} N={N} K={K}", flush=True)
+    g = gen(M * 7 + N + K)
+    x = randn(g, M, K)
+    w = randn(g, N, K, scale=K ** -0.5)
+    y = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+    qm.linear(x, w, y)
+    torch.testing.assert_close(y.float(), x.float() @ w.float().t(), **BF16)
+
