@@ -1642,11 +1642,13 @@ int make_plan(int B, int H, int Hkv, int D, int block_size, int max_blocks, int 
   // against 12.0, 32 pairs 14.4 (d-sliced: 16.2) against 13.3, 64 pairs
   // 17.2 against 16.8; at 128 pairs x 16k-32k keys the key-split kernel is
   // 2x faster.  So key-split from a sixteenth as many pairs as resident
-  // workgroups, or when a table holds >= 4096 keys.
+  // workgroups, or when a table holds >= 4096 keys, or for one 16-row tile
+  // of query rows (decode-shaped calls: at 8 pairs x 1.25k keys and 2 or 4
+  // rows per pair, 8.0 us against 9.4 for the d-sliced kernel and its merge).
   const int64_t ks_slots = (int64_t)cus * (8 / kKsWaves);  // resident workgroups
   const bool ks_fits = p->MT <= 3 && block_size >= 16 && max_blocks <= kMaxSplitPages &&
                        (pairs <= kMaxCounterPairs || (kv_split_tokens == 0 && pairs >= ks_slots));
-  const bool ks_wins = kv_split_tokens > 0 || pairs * 16 >= ks_slots || max_ctx >= 4096;
+  const bool ks_wins = kv_split_tokens > 0 || pairs * 16 >= ks_slots || max_ctx >= 4096 || p->MT == 1;
   if (dtype == NSV_BF16 && ks_fits && ks_wins) {
     // key-split kernel: each sequence's keys evenly over about CUs / pairs
     // splits (none when the pairs alone cover the chip), but no split
