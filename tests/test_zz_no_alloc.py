@@ -33,7 +33,7 @@ def _call(vb, allocation_free):
 CASES = {
     # (kernel family, first input, second smaller input)
     "key-split": (dict(ctx=[5000, 3001], q=[9, 9], H=32), dict(ctx=[4100], q=[9], H=32)),
-    "d-sliced": (dict(ctx=[1248], q=[9], H=16), dict(ctx=[700], q=[5], H=16)),
+    "d-sliced": (dict(ctx=[1248], q=[9], H=16), dict(ctx=[700], q=[9], H=16)),  # 18 rows: two 16-row tiles
     "fp32": (dict(ctx=[1248, 300], q=[9, 9], H=16, dtype="f32"), dict(ctx=[900], q=[9], H=16, dtype="f32")),
 }
 
