@@ -385,7 +385,10 @@ int nsv_linear_ss_rows(int M, int N, int K, int has_norm);
  * compute units (cus <= 0: the current device): output columns per
  * workgroup (8, 16 or 32), workgroups per 16-column tile that split the
  * reduction (> 1 only with 16-column tiles), and whether half-size
- * reduction chunks are used.  Host-only query, launches nothing; no
+ * reduction chunks are used (1), or 16-column tiles streamed whole by
+ * single waves over activations staged in LDS (2: a plain projection with
+ * at least 32 tiles per compute unit, K of 1024, 2048 or 4096 and
+ * M (K + 8) bf16 within 160 KiB, such as the LM head).  Host-only query, launches nothing; no
  * reference counterpart (it exposes this library's tiling for tests and
  * tuning). */
 int nsv_linear_plan(int M, int N, int K, int has_norm, int epilogue, int cus,

@@ -759,7 +759,14 @@ size_t nsv_linear_workspace_size(int M, int N, int K) {
 int nsv_linear_plan(int M, int N, int K, int has_norm, int epilogue, int cus, int* tile_cols, int* splits,
                     int* half_chunks) {
   if (M <= 0 || N <= 0 || K <= 0 || epilogue < 0 || epilogue > 2 || N % kBN || K % 8) return NSV_ERR_ARG;
-  const LinPlan p = linear_plan(M, N, K, has_norm != 0, epilogue, cus > 0 ? cus : lin_device_cus());
+  const int c = cus > 0 ? cus : lin_device_cus();
+  if (stream_wide(M, N, K, has_norm != 0, epilogue, c)) {  // whole 16-row weight tiles per wave
+    if (tile_cols) *tile_cols = kBN;
+    if (splits) *splits = 1;
+    if (half_chunks) *half_chunks = 2;
+    return NSV_OK;
+  }
+  const LinPlan p = linear_plan(M, N, K, has_norm != 0, epilogue, c);
   if (tile_cols) *tile_cols = p.cols;
   if (splits) *splits = p.ks;
   if (half_chunks) *half_chunks = p.small ? 1 : 0;

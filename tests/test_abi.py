@@ -226,6 +226,20 @@ def test_linear_split_only_with_16_column_tiles():
     assert {(8, False), (16, False), (16, True), (32, False)} <= seen
 
 
+def test_linear_plan_streams_wide_heads():
+    """A vocabulary-wide plain projection streams whole tiles per wave
+    (half_chunks 2) while its activations fit the LDS; past that, or with a
+    prologue or epilogue, the tiled kernels."""
+    assert linear_plan(9, 151936, 1024, False, 0, 256) == (16, 1, 2)
+    assert linear_plan(72, 151936, 1024, False, 0, 256) == (16, 1, 2)
+    assert linear_plan(19, 151936, 4096, False, 0, 256) == (16, 1, 2)
+    assert linear_plan(80, 151936, 1024, False, 0, 256)[2] != 2   # 80 x 1032 bf16 > 160 KiB
+    assert linear_plan(20, 151936, 4096, False, 0, 256)[2] != 2
+    assert linear_plan(9, 151936, 1024, True, 0, 256)[2] != 2    # RMSNorm prologue
+    assert linear_plan(9, 151936, 1536, False, 0, 256)[2] != 2   # K outside {1024, 2048, 4096}
+    assert linear_plan(9, 4096, 1024, False, 0, 256)[2] != 2     # 256 tiles: too few per CU
+
+
 def test_linear_plan_rejects_bad_shapes():
     import ctypes
     x = ctypes.c_int()
