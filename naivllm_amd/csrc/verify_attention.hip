@@ -22,8 +22,9 @@
 //     combines the partials, exchanged with agent-scope loads and stores);
 //   * d-sliced (verify_attn_bf16_kernel): workgroup = (pair, head-dim slice,
 //     key split); every slice recomputes the scores and reads the pair's K
-//     through its own L1 (shared in L2); splits, when used, merge in a
-//     second kernel.
+//     through its own L1 (shared in L2); the key splits of a slice, when
+//     used, merge in-kernel like the key-split kernel's (the last of them to
+//     finish), or in a second kernel past the arrival counters' capacity.
 // The fp32 kernel (the 1e-5 contract) uses VALU dot products.
 
 #include "common.h"
@@ -93,6 +94,7 @@ struct VerifyArgs {
   int dqc;           // head-dim slices per pair (d-sliced bf16 kernel)
   int ks_splits;     // key-split kernel: splits per sequence when split_tokens == 0
   int m_base;        // fp32 kernel: first query row (of the Mv) this launch serves
+  int dmerge;        // d-sliced kernel: the pair's last workgroup merges its splits in-kernel (else a merge launch)
 };
 
 __device__ __forceinline__ u32x4 load16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
@@ -256,6 +258,7 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
   __shared__ float row_l[MP];
   __shared__ float row_ms[MP];
   __shared__ int row_pos[MP];
+  __shared__ int ds_last;
   // PARK: each wave parks its unscaled O slice and (max, sum) in LDS of its
   // own as soon as its tiles are done, while slower waves still stream; one
   // barrier later every output is the factor-weighted sum of the parked
@@ -583,6 +586,87 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
     }
   }
   const int64_t pbase = ((int64_t)pair * a.S + split) * a.Mv;
+  // split partials with the agent-scope cache policy (this split's rows)
+  const __amdgpu_buffer_rsrc_t prs = block_rsrc(a.part_o + pbase * DH);
+  // ---- in-kernel split merge, per head-dim slice: the nsplit workgroups of
+  // a (pair, slice) count in after their partials are acknowledged (each
+  // writes its split's (max, sum), identical across slices); the last one
+  // combines the splits' partials of its slice, in split order (the result
+  // does not depend on which came last), with the ordering protocol of the
+  // key-split kernel's merge
+  auto merge_splits = [&]() {
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    const int slot = counter_slot(pair * a.dqc + dq);
+    if (tid == 0)
+      ds_last = __hip_atomic_fetch_add(&a.counters[slot], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                (unsigned)(nsplit - 1);
+    __syncthreads();
+    if (!uniform(ds_last)) return;
+    if (tid == 0) __hip_atomic_store(&a.counters[slot], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const int64_t base0 = (int64_t)pair * a.S * a.Mv;  // row 0 of split 0
+    const __amdgpu_buffer_rsrc_t ors = block_rsrc(a.part_o + base0 * DH);
+    const __amdgpu_buffer_rsrc_t mrs = block_rsrc(a.part_ml + base0 * 2);
+    constexpr int C4 = DC / 4;
+    constexpr int ITEMS = (MP * C4 + NT - 1) / NT;  // (row, 4 dims of this slice) items per thread
+    constexpr int CW = ITEMS <= 2 ? 8 : 4;          // splits whose values one round trip loads
+    bool iok[ITEMS];
+    unsigned ioff[ITEMS], imlo[ITEMS];
+    uint2* idst[ITEMS];
+    float M[ITEMS], den[ITEMS];
+    f32x4 num[ITEMS];
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+      const int qd = tid + j * NT;
+      int m = qd / C4;
+      const int c4 = qd - m * C4;
+      const int g = m / a.QL, t = m - g * a.QL;
+      const bool ok = m < a.Mv && t < qlen;
+      iok[j] = ok;
+      m = ok ? m : 0;  // (items past the rows load row 0 and are discarded)
+      ioff[j] = (unsigned)(m * DH + dq * DC + c4 * 4) * 4u;
+      imlo[j] = (unsigned)m * 8u;
+      idst[j] = reinterpret_cast<uint2*>((bf16_t*)a.out +
+                                         ((int64_t)(q0 + (ok ? t : 0)) * a.H + hk * a.Gs + a.g0 + (ok ? g : 0)) * DH +
+                                         dq * DC + c4 * 4);
+      M[j] = kNegInf;
+      den[j] = 0.f;
+      num[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int s0 = 0; s0 < nsplit; s0 += CW) {
+      float2 ml[ITEMS][CW];
+      f32x4 op[ITEMS][CW];
+#pragma unroll
+      for (int k = 0; k < CW; ++k) {
+        const unsigned rows = (unsigned)(uniform(min(s0 + k, nsplit - 1)) * a.Mv);  // past nsplit: weight 0 below
+#pragma unroll
+        for (int j = 0; j < ITEMS; ++j) {
+          ml[j][k] = load8_agent(mrs, imlo[j], rows * 8u);
+          op[j][k] = load16_agent(ors, ioff[j], rows * (DH * 4u));
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < ITEMS; ++j)
+#pragma unroll
+        for (int k = 0; k < CW; ++k) {
+          const float ms = ml[j][k].x + (s0 + k < nsplit ? 0.f : kNegInf);  // stored maxima are finite or -inf
+          const float Mn = fmaxf(M[j], ms);
+          const float ref = Mn == kNegInf ? 0.f : Mn;
+          const float a0 = __builtin_amdgcn_exp2f(M[j] - ref), a1 = __builtin_amdgcn_exp2f(ms - ref);
+          den[j] = den[j] * a0 + ml[j][k].y * a1;
+          num[j] = num[j] * a0 + op[j][k] * a1;
+          M[j] = Mn;
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < ITEMS; ++j) {
+      if (!iok[j]) continue;
+      const float inv = den[j] > 0.f ? 1.f / den[j] : 0.f;
+      const uint32_t lo = (uint32_t)f32_to_bf16_bits(num[j][0] * inv) | ((uint32_t)f32_to_bf16_bits(num[j][1] * inv) << 16);
+      const uint32_t hi = (uint32_t)f32_to_bf16_bits(num[j][2] * inv) | ((uint32_t)f32_to_bf16_bits(num[j][3] * inv) << 16);
+      *idst[j] = make_uint2(lo, hi);
+    }
+  };
   if constexpr (PARK) {
     // lane (g4, c) element i of tile (dt, mt) is O[16*mt + c][16*dt + 4*g4 + i]
 #pragma unroll
@@ -616,10 +700,10 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
         *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
       } else {
         if (row_pos[m] < 0) o = f32x4{0.f, 0.f, 0.f, 0.f};
-        *reinterpret_cast<f32x4*>(&a.part_o[(pbase + m) * DH + dq * DC + c4 * 4]) = o;
+        store16_agent(prs, (unsigned)(m * DH + dq * DC + c4 * 4) * 4u, o);
       }
     }
-    if (nsplit > 1 && dq == 0 && tid < a.Mv) {
+    if (nsplit > 1 && (dq == 0 || a.dmerge) && tid < a.Mv) {
       float M = kNegInf;
 #pragma unroll
       for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, red_m[ww][tid]);
@@ -627,9 +711,10 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
       float L = 0.f;
 #pragma unroll
       for (int ww = 0; ww < NW; ++ww) L += red_l[ww][tid] * __builtin_amdgcn_exp2f((red_m[ww][tid] - ref) * sc);
-      a.part_ml[(pbase + tid) * 2 + 0] = row_pos[tid] >= 0 && M != kNegInf ? M * sc : kNegInf;
-      a.part_ml[(pbase + tid) * 2 + 1] = row_pos[tid] >= 0 ? L : 0.f;
+      store_agent(reinterpret_cast<uint64_t*>(&a.part_ml[(pbase + tid) * 2]),
+                  row_pos[tid] >= 0 && M != kNegInf ? M * sc : kNegInf, row_pos[tid] >= 0 ? L : 0.f);
     }
+    if (nsplit > 1 && a.dmerge) merge_splits();
     return;
   }
   __syncthreads();  // also: every wave is done with its V staging rows
@@ -684,14 +769,14 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
         *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
       } else {
         if (row_pos[m] < 0) o = f32x4{0.f, 0.f, 0.f, 0.f};
-        *reinterpret_cast<f32x4*>(&a.part_o[(pbase + m) * DH + dq * DC + c4 * 4]) = o;
+        store16_agent(prs, (unsigned)(m * DH + dq * DC + c4 * 4) * 4u, o);
       }
     }
   }
-  if (nsplit > 1 && dq == 0 && tid < a.Mv) {
-    a.part_ml[(pbase + tid) * 2 + 0] = row_pos[tid] >= 0 ? row_ms[tid] : kNegInf;
-    a.part_ml[(pbase + tid) * 2 + 1] = row_pos[tid] >= 0 ? row_l[tid] : 0.f;
-  }
+  if (nsplit > 1 && (dq == 0 || a.dmerge) && tid < a.Mv)
+    store_agent(reinterpret_cast<uint64_t*>(&a.part_ml[(pbase + tid) * 2]), row_pos[tid] >= 0 ? row_ms[tid] : kNegInf,
+                row_pos[tid] >= 0 ? row_l[tid] : 0.f);
+  if (nsplit > 1 && a.dmerge) merge_splits();
 }
 
 // ---------------------------------------------------------------------------
@@ -1953,7 +2038,7 @@ int launch_verify(const VerifyArgs& a, const Plan& p, int D, int dtype, hipStrea
     }
   }
   rc = nsv_launch_status();
-  if (rc != NSV_OK || p.S <= 1 || (dtype == NSV_BF16 && p.ks)) return rc;  // key-split merges in-kernel
+  if (rc != NSV_OK || p.S <= 1 || (dtype == NSV_BF16 && (p.ks || a.dmerge))) return rc;  // merged in-kernel
   const dim3 mgrid(a.npairs, (p.Mv + 3) / 4);
   if (dtype == NSV_BF16) {
     if (D == 128) hipLaunchKernelGGL((verify_merge_kernel<bf16_t, 2>), mgrid, dim3(256), 0, s, a);
@@ -2047,6 +2132,9 @@ int nsv_verify_attention(void* out, const void* q, const void* k_cache, const vo
   a.dqc = p.dqc;
   a.ks_splits = p.ks_splits;
   a.m_base = 0;
+  // the d-sliced kernel merges its key splits in-kernel while every pair has
+  // an arrival counter of its own, else in a second launch
+  a.dmerge = dtype == NSV_BF16 && !p.ks && p.S > 1 && (int64_t)B * Hkv * p.dqc <= kMaxCounterPairs;
 
   hipStream_t s = (hipStream_t)stream;
   // one launch (and merge) per subset of each kv head's query heads; they
