@@ -369,7 +369,9 @@ __global__ __launch_bounds__(kLinThreads, lin_waves_per_eu(MT, SMALL, BNV)) void
         for (int e = 0; e < 4; ++e) v[e] += w8[ww][e];
     }
     const __amdgpu_buffer_rsrc_t prs = block_rsrc(a.part + (int64_t)tile * a.ks * (kMaxRows * kBN));
-    const unsigned ioff = (unsigned)(m * kBN + 4 * q) * 4u;             // the item in one split's block
+    // the item in one split's block (threads past the tile's items load item 0: their loads stay inside
+    // the block, which ends 80 rows x 16 columns after its start)
+    const unsigned ioff = item ? (unsigned)(m * kBN + 4 * q) * 4u : 0u;
     constexpr unsigned kSplitBytes = kMaxRows * kBN * 4u;                  // one split's block
     if (item) store16_agent(prs, ioff + (unsigned)kz * kSplitBytes, v);
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
