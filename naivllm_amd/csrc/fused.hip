@@ -22,26 +22,37 @@ __device__ __forceinline__ float bf(uint16_t b) { return bf16_bits_to_f32(b); }
 // ---------------------------------------------------------------------------
 constexpr int kNormThreads = 256;
 
+template <int J>  // elements per thread: E <= 256 J
 __global__ __launch_bounds__(kNormThreads) void rms_norm_residual_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ residual, uint16_t* __restrict__ residual_out,
     const uint16_t* __restrict__ w, uint16_t* __restrict__ out, int E, float eps) {
   __shared__ float red[kNormThreads / 64];
   const int64_t row = blockIdx.x;
   const uint16_t* xr = x + row * E;
-  const uint16_t* rr = residual ? residual + row * E : nullptr;
+  const uint16_t* rr = residual ? residual + row * E : xr;
   float ss = 0.f;
-  // thread t handles elements t, t + 256, ... (E <= 16 * 256), kept in registers
-  float v[16];
+  // thread t handles elements t, t + 256, ... (E <= J * 256), kept in
+  // registers; every load (the norm weight's included) is issued before the
+  // first is used, elements past E reading element E - 1 (one round trip)
+  uint16_t xv[J], rv[J], wv[J];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
+  for (int j = 0; j < J; ++j) {
+    const int i = min((int)threadIdx.x + j * kNormThreads, E - 1);
+    xv[j] = xr[i];
+    rv[j] = rr[i];
+    wv[j] = w[i];
+  }
+  // (used here, so that no load is moved into the residual branch below)
+#pragma unroll
+  for (int j = 0; j < J; ++j) __asm__ volatile("" ::"v"((uint32_t)rv[j]));
+  float v[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) {
     const int i = threadIdx.x + j * kNormThreads;
-    v[j] = 0.f;
-    if (i < E) {
-      float r = bf(xr[i]);
-      if (rr) r = bf16_bits_to_f32(f32_to_bf16_bits(r + bf(rr[i])));  // the residual stream is bf16
-      v[j] = r;
-      ss += r * r;
-    }
+    float r = bf(xv[j]);
+    if (residual) r = bf16_bits_to_f32(f32_to_bf16_bits(r + bf(rv[j])));  // the residual stream is bf16
+    v[j] = i < E ? r : 0.f;
+    ss += v[j] * v[j];
   }
   ss = wave_sum(ss);
   if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
@@ -51,11 +62,11 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_residual_kernel(
   for (int i = 0; i < kNormThreads / 64; ++i) tot += red[i];
   const float inv = rsqrtf(tot / (float)E + eps);
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
+  for (int j = 0; j < J; ++j) {
     const int i = threadIdx.x + j * kNormThreads;
     if (i < E) {
       if (residual_out) residual_out[row * E + i] = f32_to_bf16_bits(v[j]);
-      out[row * E + i] = f32_to_bf16_bits(v[j] * inv * bf(w[i]));
+      out[row * E + i] = f32_to_bf16_bits(v[j] * inv * bf(wv[j]));
     }
   }
 }
@@ -68,6 +79,7 @@ __global__ __launch_bounds__(kNormThreads) void rms_norm_residual_kernel(
 // row 0, as the reference's lookup does on one GPU (the id times its in-range
 // mask, layers/embedding_head.py:49-55).  One workgroup per row.
 // ---------------------------------------------------------------------------
+template <int J>  // elements per thread: E <= 256 J
 __global__ __launch_bounds__(kNormThreads) void embed_norm_kernel(
     const int64_t* __restrict__ ids, const uint16_t* __restrict__ embed, int64_t V, const uint16_t* __restrict__ w,
     uint16_t* __restrict__ residual_out, uint16_t* __restrict__ out, int E, float eps,
@@ -75,20 +87,28 @@ __global__ __launch_bounds__(kNormThreads) void embed_norm_kernel(
     float* __restrict__ rope_out) {
   __shared__ float red[kNormThreads / 64];
   const int64_t row = blockIdx.x;
+  // first round trip: the id, the position and the norm weight (elements past
+  // E read element E - 1); then the embedding row and the rotary row
   const int64_t id = ids[row];
+  const int64_t pos_raw = rope_out ? positions[row] : 0;
+  uint16_t wv[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) wv[j] = w[min((int)threadIdx.x + j * kNormThreads, E - 1)];
   const bool valid = id >= 0 && id < V;
   const uint16_t* xr = embed + (valid ? id : 0) * E;
+  uint16_t xv[J];
+#pragma unroll
+  for (int j = 0; j < J; ++j) xv[j] = xr[min((int)threadIdx.x + j * kNormThreads, E - 1)];
   if (rope_out) {
-    int64_t pos = positions[row];
-    pos = pos < 0 ? 0 : (pos >= max_pos ? max_pos - 1 : pos);
+    const int64_t pos = pos_raw < 0 ? 0 : (pos_raw >= max_pos ? max_pos - 1 : pos_raw);
     for (int i = threadIdx.x; i < D; i += kNormThreads) rope_out[row * D + i] = cos_sin[pos * D + i];
   }
   float ss = 0.f;
-  float v[16];  // thread t holds elements t, t + 256, ... (E <= 16 * 256)
+  float v[J];  // thread t holds elements t, t + 256, ...
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
+  for (int j = 0; j < J; ++j) {
     const int i = threadIdx.x + j * kNormThreads;
-    v[j] = i < E ? bf(xr[i]) : 0.f;
+    v[j] = i < E ? bf(xv[j]) : 0.f;
     ss += v[j] * v[j];
   }
   ss = wave_sum(ss);
@@ -99,11 +119,11 @@ __global__ __launch_bounds__(kNormThreads) void embed_norm_kernel(
   for (int i = 0; i < kNormThreads / 64; ++i) tot += red[i];
   const float inv = rsqrtf(tot / (float)E + eps);
 #pragma unroll
-  for (int j = 0; j < 16; ++j) {
+  for (int j = 0; j < J; ++j) {
     const int i = threadIdx.x + j * kNormThreads;
     if (i < E) {
       residual_out[row * E + i] = f32_to_bf16_bits(v[j]);
-      out[row * E + i] = f32_to_bf16_bits(v[j] * inv * bf(w[i]));
+      out[row * E + i] = f32_to_bf16_bits(v[j] * inv * bf(wv[j]));
     }
   }
 }
@@ -214,9 +234,15 @@ int nsv_rms_norm(const void* x, const void* residual, void* residual_out, const 
   if (T < 0 || E <= 0 || E > 16 * kNormThreads) return NSV_ERR_ARG;
   if (T == 0) return NSV_OK;
   if (!x || !weight || !out) return NSV_ERR_ARG;
-  hipLaunchKernelGGL(rms_norm_residual_kernel, dim3(T), dim3(kNormThreads), 0, (hipStream_t)stream,
-                     (const uint16_t*)x, (const uint16_t*)residual, (uint16_t*)residual_out, (const uint16_t*)weight,
-                     (uint16_t*)out, E, eps);
+  const int J = (E + kNormThreads - 1) / kNormThreads;
+#define NSV_NORM(JJ)                                                                                              \
+  hipLaunchKernelGGL(rms_norm_residual_kernel<JJ>, dim3(T), dim3(kNormThreads), 0, (hipStream_t)stream,          \
+                     (const uint16_t*)x, (const uint16_t*)residual, (uint16_t*)residual_out,                     \
+                     (const uint16_t*)weight, (uint16_t*)out, E, eps)
+  if (J <= 4) NSV_NORM(4);
+  else if (J <= 8) NSV_NORM(8);
+  else NSV_NORM(16);
+#undef NSV_NORM
   return nsv_launch_status();
 }
 
@@ -227,9 +253,15 @@ int nsv_embed_rms_norm(const int64_t* ids, const void* embed, int64_t vocab, con
   if (T == 0) return NSV_OK;
   if (!ids || !embed || !weight || !residual_out || !out) return NSV_ERR_ARG;
   if (rope_out && (!positions || !cos_sin || max_pos <= 0 || D <= 0)) return NSV_ERR_ARG;
-  hipLaunchKernelGGL(embed_norm_kernel, dim3(T), dim3(kNormThreads), 0, (hipStream_t)stream, ids,
-                     (const uint16_t*)embed, (int64_t)vocab, (const uint16_t*)weight, (uint16_t*)residual_out,
-                     (uint16_t*)out, E, eps, positions, cos_sin, max_pos, D, rope_out);
+  const int J = (E + kNormThreads - 1) / kNormThreads;
+#define NSV_EMB(JJ)                                                                                              \
+  hipLaunchKernelGGL(embed_norm_kernel<JJ>, dim3(T), dim3(kNormThreads), 0, (hipStream_t)stream, ids,           \
+                     (const uint16_t*)embed, (int64_t)vocab, (const uint16_t*)weight, (uint16_t*)residual_out,  \
+                     (uint16_t*)out, E, eps, positions, cos_sin, max_pos, D, rope_out)
+  if (J <= 4) NSV_EMB(4);
+  else if (J <= 8) NSV_EMB(8);
+  else NSV_EMB(16);
+#undef NSV_EMB
   return nsv_launch_status();
 }
 
