@@ -398,6 +398,22 @@ int nsv_linear(const void* x, const void* norm_w, const float* ss_in,
                void* resid, float* ss_out, int M, int N, int K,
                int epilogue, void* workspace, size_t workspace_bytes,
                void* stream);
+/* nsv_linear for decode-shaped calls of at most 2 rows (a drafter's steps):
+ * one wave per output column (per gate/up pair with epilogue 1), the whole
+ * reduction in that wave, every load in one round trip, no workspace.  Same
+ * operations per output as nsv_linear (W' = bf16(W * norm_w) with the
+ * RMSNorm prologue, one bf16 rounding per product, the same epilogues); the
+ * reduction order differs, so outputs may differ from nsv_linear's in the
+ * last bf16 place.  K in {1024, 2048, 3072, 4096}; nss_in <= 256.  The
+ * residual epilogue writes nsv_linear_decode_ss_rows(M, N) = N / 4 partial
+ * sums per row (one per 4 columns), the nss_in of the consumer.  No
+ * reference counterpart: the drafter's few-row path of this library's
+ * forward (layers/linear.py's projections at one or two rows). */
+int nsv_linear_decode(const void* x, const void* norm_w, const float* ss_in,
+                      int nss_in, float eps, const void* weight, void* y,
+                      void* resid, float* ss_out, int M, int N, int K,
+                      int epilogue, void* stream);
+int nsv_linear_decode_ss_rows(int M, int N);
 
 #ifdef __cplusplus
 }

@@ -744,6 +744,162 @@ int launch_stream_k(const StreamArgs& a, int cus, hipStream_t s) {
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// Decode-shaped projection (at most kDecodeRows rows, e.g. a drafter's one or
+// two rows per sequence): one wave per output column (SwiGLU: per gate/up
+// row pair), the whole reduction in that wave -- its weight row, the
+// activation rows and (RMSNorm prologue) the norm weight and the producer's
+// partial sums all loaded in one round trip, fp32 dot products on the VALU
+// summed across the wave with DPP, and the epilogue in the same wave.  No
+// LDS staging, no cross-wave reduction (except the residual epilogue's
+// partial sums of squares, one per workgroup of 4 columns).  The operations
+// per output are those of the tiled kernel (W' = bf16(W * norm_w), one bf16
+// rounding of each product, the same epilogues); the reduction order is its
+// own.
+// ---------------------------------------------------------------------------
+constexpr int kDecodeRows = 2;
+constexpr int kDecodeWaves = 4;  // columns per workgroup (one partial-sum slot each with the residual epilogue)
+
+template <int EPI, bool NORM, int KL, int MR>  // KL = K / 512 16-byte chunks per lane; MR rows (<= kDecodeRows)
+__global__ __launch_bounds__(kDecodeWaves * 64) void decode_linear_kernel(LinearArgs a) {
+  __asm__ volatile("" ::"s"(a.x), "s"(a.norm_w), "s"(a.ss_in), "s"(a.nss_in), "s"(a.eps), "s"(a.w), "s"(a.y),
+                   "s"(a.resid), "s"(a.ss_out), "s"(a.M), "s"(a.N), "s"(a.K));
+  __shared__ float ssq[kDecodeWaves][MR];
+  constexpr int K = KL * 512;
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ncols = EPI == 1 ? a.N / 2 : a.N;
+  const int col_raw = blockIdx.x * kDecodeWaves + w;
+  const int col = min(col_raw, ncols - 1);  // (past the last column: read the last, store nothing)
+  const int M = a.M;
+  // ---- every load, one round trip (the residual elements first: nothing
+  // before them is waited for)
+  uint32_t rres[MR];
+  if constexpr (EPI == 2) {
+#pragma unroll
+    for (int m = 0; m < MR; ++m) rres[m] = a.resid[(int64_t)min(m, M - 1) * a.N + col];
+  }
+  u32x4 wv[KL], uv[EPI == 1 ? KL : 1], xv[MR][KL], nv[NORM ? KL : 1];
+  const uint16_t* wr = a.w + (int64_t)col * K + lane * 8;
+#pragma unroll
+  for (int i = 0; i < KL; ++i) wv[i] = *reinterpret_cast<const u32x4*>(wr + i * 512);
+  if constexpr (EPI == 1) {
+    const uint16_t* ur = a.w + (int64_t)(a.N / 2 + col) * K + lane * 8;
+#pragma unroll
+    for (int i = 0; i < KL; ++i) uv[i] = *reinterpret_cast<const u32x4*>(ur + i * 512);
+  }
+#pragma unroll
+  for (int m = 0; m < MR; ++m)
+#pragma unroll
+    for (int i = 0; i < KL; ++i)
+      xv[m][i] = *reinterpret_cast<const u32x4*>(a.x + (int64_t)min(m, M - 1) * K + i * 512 + lane * 8);
+  float ssv[NORM ? MR : 1][4];
+  if constexpr (NORM) {
+#pragma unroll
+    for (int i = 0; i < KL; ++i) nv[i] = *reinterpret_cast<const u32x4*>(a.norm_w + i * 512 + lane * 8);
+    // slots lane, lane + 64, ... of each row (at most 256 slots: the host's bound)
+#pragma unroll
+    for (int m = 0; m < MR; ++m)
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        ssv[m][u] = a.ss_in[(int64_t)min(lane + 64 * u, a.nss_in - 1) * a.M + min(m, M - 1)];
+  }
+  __builtin_amdgcn_sched_barrier(0);  // (every load above is issued before any of them is used)
+  // (used here, so that no load is moved under the selects and branches below)
+  if constexpr (NORM) {
+#pragma unroll
+    for (int m = 0; m < MR; ++m) __asm__ volatile("" ::"v"(ssv[m][0]), "v"(ssv[m][1]), "v"(ssv[m][2]), "v"(ssv[m][3]));
+  }
+  if constexpr (EPI == 2) {
+#pragma unroll
+    for (int m = 0; m < MR; ++m) __asm__ volatile("" ::"v"(rres[m]));
+  }
+  // ---- dot products: lane holds elements 512 i + 8 lane .. + 7
+  auto dot = [&](const u32x4 (&wrow)[KL], int m) {
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < KL; ++i)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          float wf = bfv(wrow[i][q], h);
+          if constexpr (NORM) wf = bf16_bits_to_f32(f32_to_bf16_bits(wf * bfv(nv[i][q], h)));
+          acc = fmaf(bfv(xv[m][i][q], h), wf, acc);
+        }
+    return wave_sum(acc);
+  };
+  float inv[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) {
+    inv[m] = 1.f;
+    if constexpr (NORM) {
+      float t = 0.f;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) t += lane + 64 * u < a.nss_in ? ssv[m][u] : 0.f;
+      inv[m] = rsqrtf(wave_sum(t) / (float)K + a.eps);
+    }
+  }
+  const bool live = col_raw < ncols;  // uniform
+  if constexpr (EPI == 1) {
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      const float g = bf16_bits_to_f32(f32_to_bf16_bits(dot(wv, m) * inv[m]));
+      const float u = bf16_bits_to_f32(f32_to_bf16_bits(dot(uv, m) * inv[m]));
+      if (live && lane == 0 && m < M) a.y[(int64_t)m * ncols + col] = f32_to_bf16_bits(g / (1.f + __expf(-g)) * u);
+    }
+  } else {
+    float ssm[MR];
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+      float v = bf16_bits_to_f32(f32_to_bf16_bits(dot(wv, m) * inv[m]));
+      ssm[m] = 0.f;
+      if constexpr (EPI == 2) {
+        v = bf16_bits_to_f32(f32_to_bf16_bits(v + bf16_bits_to_f32(rres[m] & 0xffffu)));  // the residual stream is bf16
+        ssm[m] = live ? v * v : 0.f;
+        if (live && lane == 0 && m < M) a.resid[(int64_t)m * a.N + col] = f32_to_bf16_bits(v);
+      } else {
+        if (live && lane == 0 && m < M) a.y[(int64_t)m * a.N + col] = f32_to_bf16_bits(v);
+      }
+    }
+    if constexpr (EPI == 2) {
+      // the workgroup's 4 columns: one partial sum of squares per row, added in wave order
+      if (lane == 0) {
+#pragma unroll
+        for (int m = 0; m < MR; ++m) ssq[w][m] = ssm[m];
+      }
+      __syncthreads();
+      if (threadIdx.x < MR && (int)threadIdx.x < M) {
+        const int m = threadIdx.x;
+        float t = 0.f;
+#pragma unroll
+        for (int ww = 0; ww < kDecodeWaves; ++ww) t += ssq[ww][m];
+        a.ss_out[(int64_t)blockIdx.x * a.M + m] = t;
+      }
+    }
+  }
+}
+
+template <int EPI, bool NORM, int KL>
+int launch_decode_k(const LinearArgs& a, hipStream_t s) {
+  const int ncols = EPI == 1 ? a.N / 2 : a.N;
+  const dim3 grid((ncols + kDecodeWaves - 1) / kDecodeWaves);
+  if (a.M <= 1) hipLaunchKernelGGL((decode_linear_kernel<EPI, NORM, KL, 1>), grid, dim3(kDecodeWaves * 64), 0, s, a);
+  else hipLaunchKernelGGL((decode_linear_kernel<EPI, NORM, KL, 2>), grid, dim3(kDecodeWaves * 64), 0, s, a);
+  return nsv_launch_status();
+}
+
+template <int EPI, bool NORM>
+int launch_decode(const LinearArgs& a, hipStream_t s) {
+  switch (a.K / 512) {
+    case 2: return launch_decode_k<EPI, NORM, 2>(a, s);
+    case 4: return launch_decode_k<EPI, NORM, 4>(a, s);
+    case 6: return launch_decode_k<EPI, NORM, 6>(a, s);
+    default: return launch_decode_k<EPI, NORM, 8>(a, s);
+  }
+}
+
 }  // namespace
 
 extern "C" {
@@ -773,6 +929,41 @@ int nsv_linear_plan(int M, int N, int K, int has_norm, int epilogue, int cus, in
   if (splits) *splits = p.ks;
   if (half_chunks) *half_chunks = p.small ? 1 : 0;
   return NSV_OK;
+}
+
+int nsv_linear_decode_ss_rows(int M, int N) {
+  if (M <= 0 || M > kDecodeRows || N <= 0 || N % kBN) return 0;
+  return (N + kDecodeWaves - 1) / kDecodeWaves;
+}
+
+int nsv_linear_decode(const void* x, const void* norm_w, const float* ss_in, int nss_in, float eps, const void* weight,
+                      void* y, void* resid, float* ss_out, int M, int N, int K, int epilogue, void* stream) {
+  if (M < 0 || N <= 0 || K <= 0 || epilogue < 0 || epilogue > 2) return NSV_ERR_ARG;
+  if (M == 0) return NSV_OK;
+  if (M > kDecodeRows || N % kBN || (K != 1024 && K != 2048 && K != 3072 && K != 4096)) return NSV_ERR_UNSUPPORTED;
+  if (!x || !weight) return NSV_ERR_ARG;
+  if (norm_w && (!ss_in || nss_in <= 0)) return NSV_ERR_ARG;
+  if (norm_w && nss_in > 256) return NSV_ERR_UNSUPPORTED;
+  if (epilogue == 2 ? (!resid || !ss_out) : !y) return NSV_ERR_ARG;
+  LinearArgs a{};
+  a.x = (const uint16_t*)x;
+  a.norm_w = (const uint16_t*)norm_w;
+  a.ss_in = ss_in;
+  a.nss_in = nss_in;
+  a.eps = eps;
+  a.w = (const uint16_t*)weight;
+  a.y = (uint16_t*)y;
+  a.resid = (uint16_t*)resid;
+  a.ss_out = ss_out;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.ks = 1;
+  hipStream_t s = (hipStream_t)stream;
+  const bool norm = norm_w != nullptr;
+  if (epilogue == 0) return norm ? launch_decode<0, true>(a, s) : launch_decode<0, false>(a, s);
+  if (epilogue == 1) return norm ? launch_decode<1, true>(a, s) : launch_decode<1, false>(a, s);
+  return norm ? launch_decode<2, true>(a, s) : launch_decode<2, false>(a, s);
 }
 
 int nsv_linear(const void* x, const void* norm_w, const float* ss_in, int nss_in, float eps, const void* weight,

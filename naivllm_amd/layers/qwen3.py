@@ -107,6 +107,17 @@ def qk_norm_rope_store(qkv, q_norm_w, k_norm_w, cos_sin, positions, slot_mapping
     _lib.check(rc, "qk_norm_rope_store")
 
 
+def decode_fits(hidden: int, attn_dim: int, intermediate: int) -> bool:
+    """Whether every projection's reduction suits nsv_linear_decode, and the
+    partial sums of the hidden size fit its prologue (at most 256 slots)."""
+    return all(k in (1024, 2048, 3072, 4096) for k in (hidden, attn_dim, intermediate)) and hidden // 4 <= 256
+
+
+def decode_ss_rows(M: int, N: int) -> int:
+    """Partial-sum rows a decode-shaped residual epilogue writes (nsv_linear_decode)."""
+    return int(_lib.lib().nsv_linear_decode_ss_rows(M, N))
+
+
 def ss_rows(M: int, N: int, K: int, has_norm: bool = False) -> int:
     """Rows of partial sums of r^2 a residual-epilogue linear writes (one per
     16- or 8-column tile of the output)."""
@@ -115,8 +126,11 @@ def ss_rows(M: int, N: int, K: int, has_norm: bool = False) -> int:
 
 def linear(x: torch.Tensor, weight: torch.Tensor, y: torch.Tensor | None = None, *,
            norm_w: torch.Tensor | None = None, ss_in: torch.Tensor | None = None, eps: float = 1e-6,
-           swiglu: bool = False, resid: torch.Tensor | None = None, ss_out: torch.Tensor | None = None) -> None:
-    """y = h @ weight.T on this library's few-row kernel (nsv_linear).
+           swiglu: bool = False, resid: torch.Tensor | None = None, ss_out: torch.Tensor | None = None,
+           decode: bool = False) -> None:
+    """y = h @ weight.T on this library's few-row kernel (nsv_linear), or,
+    decode=True, on its one-wave-per-column kernel for one or two rows
+    (nsv_linear_decode: ss_out then has decode_ss_rows(M, N) rows).
 
     h = rmsnorm(x) * norm_w when norm_w is given (x is then the residual
     stream and ss_in [n, M] the producer's partial sums of x^2), else x.
@@ -128,6 +142,12 @@ def linear(x: torch.Tensor, weight: torch.Tensor, y: torch.Tensor | None = None,
     epi = 2 if resid is not None else (1 if swiglu else 0)
     nss = ss_in.shape[0] if ss_in is not None else 0
     h = _lib.lib()
+    if decode:
+        rc = h.nsv_linear_decode(x.data_ptr(), _lib.ptr(norm_w), _lib.ptr(ss_in), nss, eps, weight.data_ptr(),
+                                 _lib.ptr(y), _lib.ptr(resid), _lib.ptr(ss_out), M, N, K, epi,
+                                 _lib.stream_ptr(x.device))
+        _lib.check(rc, "linear_decode")
+        return
     nbytes = h.nsv_linear_workspace_size(M, N, K)
     ws = _lib.workspace(x.device, nbytes, "linear")
     rc = h.nsv_linear(x.data_ptr(), _lib.ptr(norm_w), _lib.ptr(ss_in), nss, eps, weight.data_ptr(),
@@ -242,6 +262,10 @@ class Qwen3Verify:
         self.k_caches: list[torch.Tensor] = []
         self.v_caches: list[torch.Tensor] = []
         self.block_size = 0
+        # forwards of one or two rows take the one-wave-per-column projections
+        # (a drafter's steps; the target keeps one kernel family at every row
+        # count, so its rows come out the same at every batch shape)
+        self.decode_linears = False
 
     def prefill_q_block(self) -> int:
         """Query rows per causal block of a prefill: the verify kernel serves
@@ -299,19 +323,23 @@ class Qwen3Verify:
             # projection that produces it: 6 launches per layer.
             qkv = torch.empty(T, (H + 2 * Hkv) * D, dtype=self.dtype, device=self.device)
             act = torch.empty(T, I, dtype=self.dtype, device=self.device)
+            # one or two rows on a drafter: the one-wave-per-column kernel
+            dec = self.decode_linears and T <= 2 and decode_fits(E, H * D, I)
             # partial sums of resid^2 from o_proj and down (their tiles' count)
-            ss_o = torch.empty(ss_rows(T, E, H * D), T, dtype=torch.float32, device=self.device)
-            ss_d = torch.empty(ss_rows(T, E, I), T, dtype=torch.float32, device=self.device)
+            ss_o = torch.empty(decode_ss_rows(T, E) if dec else ss_rows(T, E, H * D), T, dtype=torch.float32,
+                               device=self.device)
+            ss_d = torch.empty(decode_ss_rows(T, E) if dec else ss_rows(T, E, I), T, dtype=torch.float32,
+                               device=self.device)
             for li, L in enumerate(self.layers):
                 if li == 0:
-                    linear(h, L["qkv"], qkv)
+                    linear(h, L["qkv"], qkv, decode=dec)
                 else:
-                    linear(resid, L["qkv"], qkv, norm_w=L["ln1"], ss_in=ss_d, eps=eps)
+                    linear(resid, L["qkv"], qkv, norm_w=L["ln1"], ss_in=ss_d, eps=eps, decode=dec)
                 qk_norm_rope_store(qkv, L["q_norm"], L["k_norm"], rope_rows, None, slot_mapping, q,
                                    self.k_caches[li], self.v_caches[li], H, Hkv, D, eps)
-                linear(attn(li).view(T, H * D), L["o"], resid=resid, ss_out=ss_o)
-                linear(resid, L["gate_up"], act, norm_w=L["ln2"], ss_in=ss_o, eps=eps, swiglu=True)
-                linear(act, L["down"], resid=resid, ss_out=ss_d)
+                linear(attn(li).view(T, H * D), L["o"], resid=resid, ss_out=ss_o, decode=dec)
+                linear(resid, L["gate_up"], act, norm_w=L["ln2"], ss_in=ss_o, eps=eps, swiglu=True, decode=dec)
+                linear(act, L["down"], resid=resid, ss_out=ss_d, decode=dec)
             rms_norm(resid, self.norm, eps, h)
         else:
             # wider batches: hipBLASLt projections between this library's

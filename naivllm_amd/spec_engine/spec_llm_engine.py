@@ -90,6 +90,7 @@ class SpecLLMEngine:
             if dcfg.vocab_size != cfg.vocab_size:
                 raise ValueError("draft and target models must share the tokenizer/vocabulary")
             self.draft_model = Qwen3Verify(dcfg, self.device, seed=config.get("draft_seed", seed + 1))
+            self.draft_model.decode_linears = True  # its one- and two-row steps
         K = self.num_speculative_tokens
         self.history_len = self.max_model_length + K + 1
         self.max_blocks = math.ceil(self.history_len / self.block_size)

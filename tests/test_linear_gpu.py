@@ -207,3 +207,79 @@ def test_linear_wide(M, N, K):
     qm.linear(x, w, y)
     torch.testing.assert_close(y.float(), x.float() @ w.float().t(), **BF16)
 
+
+# The decode-shaped kernel (nsv_linear_decode): one or two rows, each
+# epilogue, the Qwen3-0.6B projections and an 8B-wide reduction; the same
+# contract against the same fp32 restatements (its reduction order is its own)
+@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("N,K,norm", [(4096, 1024, False), (4096, 1024, True), (1024, 2048, False),
+                                      (6144, 4096, True)])
+def test_linear_decode_plain(M, N, K, norm):
+    print(f"case: linear decode plain M={M} N={N} K={K} norm={norm}", flush=True)
+    g = gen(M * 13 + N + K)
+    x = randn(g, M, K)
+    w = randn(g, N, K, scale=K ** -0.5)
+    y = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+    if norm:
+        nw = (1.0 + 0.3 * torch.randn(K, generator=g, device="cuda")).to(torch.bfloat16)
+        qm.linear(x, w, y, norm_w=nw, ss_in=partial_squares(x, 256), eps=1e-6, decode=True)
+        torch.testing.assert_close(y.float(), norm_linear_ref(x, nw, w, 1e-6), **BF16)
+    else:
+        qm.linear(x, w, y, decode=True)
+        torch.testing.assert_close(y.float(), x.float() @ w.float().t(), **BF16)
+
+
+@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("I,K,norm", [(3072, 1024, True), (3072, 1024, False)])
+def test_linear_decode_swiglu(M, I, K, norm):
+    print(f"case: linear decode swiglu M={M} I={I} K={K} norm={norm}", flush=True)
+    g = gen(M + I + K + 5)
+    r = randn(g, M, K)
+    w = randn(g, 2 * I, K, scale=K ** -0.5)
+    y = torch.full((M, I), float("nan"), dtype=torch.bfloat16, device="cuda")
+    if norm:
+        nw = (1.0 + 0.3 * torch.randn(K, generator=g, device="cuda")).to(torch.bfloat16)
+        qm.linear(r, w, y, norm_w=nw, ss_in=partial_squares(r, 64), eps=1e-6, swiglu=True, decode=True)
+        gu = norm_linear_ref(r, nw, w, 1e-6).to(torch.bfloat16).float()
+    else:
+        qm.linear(r, w, y, swiglu=True, decode=True)
+        gu = (r.float() @ w.float().t()).to(torch.bfloat16).float()
+    torch.testing.assert_close(y.float(), F.silu(gu[:, :I]) * gu[:, I:], **BF16)
+
+
+@pytest.mark.parametrize("M", [1, 2])
+@pytest.mark.parametrize("N,K", [(1024, 2048), (1024, 3072), (1040, 1024)])
+def test_linear_decode_residual(M, N, K):
+    # 1040 columns: the last workgroup holds 4 of them, as every other (N % 16 == 0)
+    print(f"case: linear decode residual M={M} N={N} K={K}", flush=True)
+    g = gen(M * 5 + N * 3 + K)
+    x = randn(g, M, K)
+    w = randn(g, N, K, scale=K ** -0.5)
+    r0 = randn(g, M, N)
+    r = r0.clone()
+    rows = qm.decode_ss_rows(M, N)
+    assert rows == N // 4
+    ss = torch.full((rows, M), float("nan"), device="cuda")
+    qm.linear(x, w, resid=r, ss_out=ss, decode=True)
+    prod = (x.float() @ w.float().t()).to(torch.bfloat16)
+    torch.testing.assert_close(r.float(), (prod.float() + r0.float()).to(torch.bfloat16).float(), **BF16)
+    torch.testing.assert_close(ss, partial_squares(r, rows), rtol=1e-5, atol=1e-5)
+
+
+def test_linear_decode_chain_feeds_prologue():
+    # o_proj's decode partial sums (N / 4 slots) feed gate_up's decode prologue
+    print("case: linear decode chain o_proj -> gate_up", flush=True)
+    g = gen(77)
+    M, E, I = 2, 1024, 3072
+    a = randn(g, M, 2048)
+    wo = randn(g, E, 2048, scale=2048 ** -0.5)
+    wgu = randn(g, 2 * I, E, scale=E ** -0.5)
+    nw = (1.0 + 0.3 * torch.randn(E, generator=g, device="cuda")).to(torch.bfloat16)
+    r = randn(g, M, E)
+    ss = torch.empty(qm.decode_ss_rows(M, E), M, device="cuda")
+    qm.linear(a, wo, resid=r, ss_out=ss, decode=True)
+    y = torch.empty(M, I, dtype=torch.bfloat16, device="cuda")
+    qm.linear(r, wgu, y, norm_w=nw, ss_in=ss, eps=1e-6, swiglu=True, decode=True)
+    gu = norm_linear_ref(r, nw, wgu, 1e-6).to(torch.bfloat16).float()
+    torch.testing.assert_close(y.float(), F.silu(gu[:, :I]) * gu[:, I:], **BF16)
+
