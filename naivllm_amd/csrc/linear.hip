@@ -79,6 +79,9 @@ __device__ __forceinline__ float bfv(uint32_t word, int hi) { return __uint_as_f
 // per lane: the small chunk (64 elements up to 32 rows, 32 beyond) keeps the
 // per-wave staging of [16 + MP rows][KC] within that.  A grid that fits the
 // CUs takes twice the chunk (half the round trips of a long reduction).
+// (4-column tiles at 9 rows with 256-element chunks, every 2048-element
+// reduction one chunk per wave issued at once: 5.80 us per o_proj/down call
+// against 5.29 with 128.)
 constexpr int lin_kc(int MT, bool small) { return (MT <= 2 ? 128 : 64) / (small ? 2 : 1); }
 
 // Minimum waves per SIMD the compiler must allow (HIP's second
@@ -98,8 +101,9 @@ constexpr int lin_waves_per_eu(int MT, bool small, int bnv) { return small && !(
 // or 32 (two 16-column MFMA tiles per wave) for wide SwiGLU projections.
 template <int MT, bool NORM, int EPI, bool SMALL, int BNV = kBN>  // EPI 0: plain, 1: SwiGLU, 2: residual
 __global__ __launch_bounds__(kLinThreads, lin_waves_per_eu(MT, SMALL, BNV)) void linear_kernel(LinearArgs a) {
-  static_assert(BNV == kBN || (BNV == 8 && EPI != 1) || (BNV == 32 && EPI == 1),
-                "8-column tiles: plain and residual epilogues; 32-column tiles: SwiGLU");
+  static_assert(BNV == kBN || (BNV == 8 && EPI != 1) || (BNV == 4 && EPI != 1 && !NORM && !SMALL) ||
+                    (BNV == 32 && EPI == 1),
+                "4- and 8-column tiles: plain and residual epilogues; 32-column tiles: SwiGLU");
   constexpr int MP = MT * 16;
   constexpr int WR = BNV > kBN ? BNV : kBN;  // staged weight rows (MFMA columns), BNV rounded up to 16
   constexpr int NTL = WR / 16;               // 16-column MFMA tiles per workgroup
@@ -458,7 +462,7 @@ __global__ __launch_bounds__(kLinThreads, lin_waves_per_eu(MT, SMALL, BNV)) void
     }
     if constexpr (EPI == 2) {
       // the QPR threads of a row are adjacent lanes of one wave: fixed-order butterfly
-      ss += __shfl_xor(ss, 1, NSV_WAVE);
+      if constexpr (QPR >= 2) ss += __shfl_xor(ss, 1, NSV_WAVE);
       if constexpr (QPR == 4) ss += __shfl_xor(ss, 2, NSV_WAVE);
       if (tid < MP * QPR && m < M && q == 0) a.ss_out[(int64_t)tile * a.M + row0 + m] = ss;
     }
@@ -489,6 +493,15 @@ int lin_device_cus() {
 // at most 31 rows, fewer than 128 16-column tiles (no split reduction then).
 bool linear_half_tiles(int M, int N, bool norm, int epi) {
   return !norm && epi != 1 && M <= 31 && N / kBN < 128 && N % 8 == 0;
+}
+
+// 4-column tiles where even 8-column tiles leave CUs idle and 4-column ones
+// still fit one workgroup per CU (full chunks, no split reduction; the MFMA
+// tile's other 12 weight rows stay zero).  Measured on MI355X (Qwen3-0.6B
+// o_proj and down, N = 1024, in the replayed verify round): 5.73 -> 5.29 us
+// per call at 9 rows (128 -> 256 workgroups), 6.80 -> 6.48 at 18.
+bool linear_quarter_tiles(int M, int N, bool norm, int epi, int cus) {
+  return linear_half_tiles(M, N, norm, epi) && N % 4 == 0 && N / 8 < cus && N / 4 <= cus;
 }
 
 // 32-column tiles (16 gate + 16 up rows) for the SwiGLU epilogue where the
@@ -534,6 +547,7 @@ struct LinPlan {
 LinPlan linear_plan(int M, int N, int K, bool norm, int epi, int cus) {
   const int gy = (M + kMaxRows - 1) / kMaxRows;
   if (linear_wide_tiles(N, epi, cus)) return {32, 1, M <= 32 && (int64_t)(N / 32) * gy > cus};
+  if (linear_quarter_tiles(M, N, norm, epi, cus)) return {4, 1, false};
   if (linear_half_tiles(M, N, norm, epi)) return {8, 1, (int64_t)(N / 8) * gy > cus};
   const int ks = linear_splits(M, N, K);
   return {16, ks, (int64_t)(N / kBN) * gy * ks > cus};
@@ -554,7 +568,7 @@ int launch_linear_tiles(const LinearArgs& a, bool norm, int epi, dim3 grid, hipS
   if constexpr (BNV == 32) {  // SwiGLU only
     if (norm) NSV_LIN(true, 1);
     else NSV_LIN(false, 1);
-  } else if constexpr (BNV == 8) {  // plain or residual, no prologue
+  } else if constexpr (BNV <= 8) {  // plain or residual, no prologue
     if (epi == 0) NSV_LIN(false, 0);
     else NSV_LIN(false, 2);
   } else if (norm) {
@@ -577,7 +591,8 @@ int launch_linear(const LinearArgs& a, const LinPlan& p, bool norm, int epi, hip
     return p.small ? launch_linear_tiles<MT, 32, true>(a, norm, epi, grid, s)
                    : launch_linear_tiles<MT, 32, false>(a, norm, epi, grid, s);
   }
-  if constexpr (MT <= 2) {  // 8-column tiles take at most 31 rows
+  if constexpr (MT <= 2) {  // 4- and 8-column tiles take at most 31 rows
+    if (p.cols == 4) return launch_linear_tiles<MT, 4, false>(a, norm, epi, grid, s);
     if (p.cols == 8) {
       return p.small ? launch_linear_tiles<MT, 8, true>(a, norm, epi, grid, s)
                      : launch_linear_tiles<MT, 8, false>(a, norm, epi, grid, s);
@@ -906,6 +921,7 @@ extern "C" {
 
 int nsv_linear_ss_rows(int M, int N, int K, int has_norm) {
   if (M <= 0 || N <= 0 || K <= 0 || N % kBN) return 0;
+  if (linear_quarter_tiles(M, N, has_norm != 0, 2, lin_device_cus())) return N / 4;
   return linear_half_tiles(M, N, has_norm != 0, 2) ? N / 8 : N / kBN;
 }
 

@@ -179,9 +179,9 @@ def test_linear_rejects_bad_arguments_before_launch():
     # split reduction (72 rows, 64 column tiles) needs the workspace; 9 rows do not
     assert h.nsv_linear_workspace_size(9, 1024, 2048) == 0
     # residual partial sums: per 8-column tile at few rows over few tiles, else per 16-column tile
-    assert h.nsv_linear_ss_rows(9, 1024, 2048, 0) == 128
+    assert h.nsv_linear_ss_rows(9, 1024, 2048, 0) == 256  # 4-column tiles (no device: 256 CUs assumed)
     assert h.nsv_linear_ss_rows(9, 1024, 2048, 1) == 64
-    assert h.nsv_linear_ss_rows(18, 1024, 2048, 0) == 128
+    assert h.nsv_linear_ss_rows(18, 1024, 2048, 0) == 256
     assert h.nsv_linear_ss_rows(36, 1024, 2048, 0) == 64
     assert h.nsv_linear_ss_rows(9, 4096, 1024, 0) == 256
     n = h.nsv_linear_workspace_size(72, 1024, 2048)
@@ -214,16 +214,18 @@ def test_linear_split_only_with_16_column_tiles():
                         for epi in (0, 1, 2):
                             cols, ks, half = linear_plan(M, N, K, norm, epi, cus)
                             seen.add((cols, ks > 1))
-                            assert cols in (8, 16, 32)
+                            assert cols in (4, 8, 16, 32)
                             if cols != 16:
                                 assert ks == 1, (cus, M, N, K, norm, epi, cols, ks)
                             if cols == 32:
                                 assert epi == 1 and N // 16 >= 128
-                            if cols == 8:
+                            if cols in (4, 8):
                                 assert not norm and epi != 1 and M <= 31
+                            if cols == 4:
+                                assert N // 4 <= cus and half == 0
                             ws = h.nsv_linear_workspace_size(M, N, K)
                             assert (ws > 0) == (ks > 1), (cus, M, N, K, ks, ws)
-    assert {(8, False), (16, False), (16, True), (32, False)} <= seen
+    assert {(4, False), (8, False), (16, False), (16, True), (32, False)} <= seen
 
 
 def test_linear_plan_streams_wide_heads():

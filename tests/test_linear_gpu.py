@@ -105,8 +105,9 @@ def test_linear_swiglu(M, I, K, norm):
     torch.testing.assert_close(y.float(), want, **BF16)
 
 
+# (4-column tiles: 1, 9, 16, 18 and 31 rows, reductions of whole and partial 128-element chunks, 1-3 per wave)
 @pytest.mark.parametrize("M,N,K", [(9, 1024, 2048), (18, 1024, 3072), (72, 1024, 3072), (100, 256, 512),
-                                   (3, 4096, 4096)])
+                                   (3, 4096, 4096), (1, 1024, 3072), (16, 1024, 1032), (31, 512, 2056)])
 def test_linear_residual(M, N, K):
     print(f"case: linear residual M={M} N={N} K={K}", flush=True)
     g = gen(M * 7 + N * 3 + K)
