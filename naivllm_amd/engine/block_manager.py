@@ -27,8 +27,11 @@ needs one (see there).
 
 ``register_full_pages`` is this build's addition for the device-resident
 round, whose tokens land on the host only when a sequence finishes: it
-hashes every full page of the final token list (the reference hashes them
-one by one in ``append`` as decoding fills them).
+hashes every page of the final token list whose KV is complete (the
+reference hashes them one by one in ``append`` as decoding fills them).
+``can_allocate`` takes an optional reservation and counts the cached hits
+that must be taken out of the free queue; ``free_pages_needed``,
+``uncached_tokens`` and ``pages_short`` are the scheduler's page arithmetic.
 """
 
 from __future__ import annotations
@@ -138,10 +141,28 @@ class BlockManager:
         return out
 
     # -------------------------------------------------------------- allocation
-    def can_allocate(self, seq) -> bool:
+    def free_pages_needed(self, seq, num_tokens: int = 0) -> int:
+        """Free pages that allocating ``seq`` with room for
+        ``max(num_tokens, len(seq))`` positions takes out of the free queue:
+        the pages the prefix cache does not serve, plus every cached hit no
+        sequence holds (it sits in the free queue until taken)."""
         seq.block_size = self.block_size
         hits = self._cached_prefix(seq)
-        return len(self.free_block_ids) >= seq.num_blocks - len(hits)
+        pages = self._pages_for(max(num_tokens, seq.num_tokens))
+        idle_hits = sum(1 for b in hits if self.blocks[b].ref_count == 0)
+        return pages - len(hits) + idle_hits
+
+    def can_allocate(self, seq, num_tokens: int = 0) -> bool:
+        """Whether ``allocate`` (then ``ensure_capacity(seq, num_tokens)``)
+        finds enough free pages.  (The reference compares the free pages with
+        the missing pages only, so a hit taken from the free queue can leave
+        ``allocate`` short.)"""
+        return len(self.free_block_ids) >= self.free_pages_needed(seq, num_tokens)
+
+    def uncached_tokens(self, seq) -> int:
+        """Prompt tokens the prefix cache does not serve (the prefill's work)."""
+        seq.block_size = self.block_size
+        return seq.num_tokens - len(self._cached_prefix(seq)) * self.block_size
 
     def allocate(self, seq) -> None:
         seq.block_size = self.block_size
@@ -207,6 +228,10 @@ class BlockManager:
         }
 
     # ------------------------------------------------------------ token growth
+    def pages_short(self, seq) -> int:
+        """Pages the sequence's table lacks for its token count."""
+        return max(0, seq.num_blocks - len(self._table(seq)))
+
     def can_append(self, seq) -> bool:
         """Whether ``append`` can give the newest token its page: a free page
         is needed exactly when the token crossed into a page the table does
@@ -243,11 +268,14 @@ class BlockManager:
             assert self.blocks[table[-1]].hash == -1, "Last block should be partial block with hash -1"
 
     def register_full_pages(self, seq) -> None:
-        """Hash every full page of the sequence's token list that has no hash
-        yet (pages filled by the device round), in order, so later requests
-        can reuse them."""
+        """Hash, in order, every page of the sequence that has no hash yet and
+        whose tokens all have their KV written, so later requests can reuse
+        it.  The device round writes a token's KV in the round after the one
+        that committed it (its verify rows are [last confirmed, drafts]), so
+        the last token never has KV of its own: a page is registered only when
+        it ends before the last token."""
         table = self._table(seq)
-        full = min(seq.num_tokens // self.block_size, len(table))
+        full = min(max(seq.num_tokens - 1, 0) // self.block_size, len(table))
         for i in range(full):
             if self.blocks[table[i]].hash == -1:
                 self._finalize_last(seq, i + 1)

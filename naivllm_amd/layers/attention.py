@@ -121,6 +121,10 @@ def paged_attention_verify(
     qlen_bound = int(max_q_len if max_q_len is not None else block_m)
     code = _lib.dtype_code(query.dtype)
     h = _lib.lib()
+    if out is not None and (tuple(out.shape) != tuple(query.shape) or out.dtype != query.dtype
+                            or out.device != query.device or not out.is_contiguous()):
+        raise ValueError(f"out must be a contiguous {query.dtype} tensor of shape {tuple(query.shape)} on "
+                         f"{query.device}")
     if allocation_free:
         if out is None:
             raise ValueError("allocation_free=True needs a preallocated out")

@@ -116,6 +116,29 @@ def test_warm_pinned_prefix_is_reused():
     eng.exit()
 
 
+@pytest.mark.parametrize("prompt_len,max_tokens", [(100, 28), (127, 1)])
+def test_output_ending_on_a_page_boundary_is_not_served_from_cache(prompt_len, max_tokens):
+    # the request ends exactly on a page boundary (128 = 2 pages of 64), so its
+    # last token has no KV; a follow-up prompt that extends it must recompute
+    # that page, and its output must equal a fresh engine's
+    print(f"case: page-boundary finish, prompt {prompt_len}, max_tokens {max_tokens}", flush=True)
+    prompt = doc_prompts(5, 1, doc_len=300)[0][:prompt_len]
+    params = SamplingParams(temperature=0, max_tokens=max_tokens, ignore_eos=True)
+    eng = SpecLLMEngine(config(seed=17))
+    first = eng.generate_token_ids([prompt], params)["token_ids"][0]
+    follow = prompt + first + [3, 1, 4, 1, 5, 9, 2, 6, 5, 3]
+    follow_params = SamplingParams(temperature=0, max_tokens=12, ignore_eos=True)
+    hits0 = eng.block_manager.cache_stats()["hits"]
+    warm = eng.generate_token_ids([follow], follow_params)
+    assert eng.block_manager.cache_stats()["hits"] - hits0 == 1  # page 0 only
+    assert warm["metrics"]["prefill_tokens"] == len(follow) - 64
+    eng.exit()
+    fresh_eng = SpecLLMEngine(config(seed=17))
+    fresh = fresh_eng.generate_token_ids([follow], follow_params)
+    fresh_eng.exit()
+    assert warm["token_ids"] == fresh["token_ids"]
+
+
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
 def test_prefill_blocks_match_whole_sequence_attention(dtype):
     # two sequences: one prefilled from token 0, one whose first 2 pages are a cached prefix
