@@ -360,6 +360,82 @@ def ceilings(wl: "Workload") -> dict:
             "stream_us": round(stream_us, 3), "stream_GBs": round(kv_bytes / stream_us / 1e3, 1)}
 
 
+STAMP_POINTS = ["entry", "metadata back", "first tile landed", "key loop done (wave 0)", "waves merged",
+                "arrival counted", "split merge done", "every wave's key loop done", "O rows in LDS"]
+
+
+def stamp_timeline(wl: "Workload", split: int, replays: int = 10) -> dict:
+    """Per-workgroup clock stamps of the verify-attention kernel (the stamped
+    library, NSV_STAMP_LIB=1), timed like the metric: the 28-call step is
+    captured as a hipGraph and replayed.  Every time is taken from the call's
+    earliest workgroup entry, in microseconds (the clock ticks every 10 ns).
+    Reported per point: the median over the workgroups that reached it, and
+    the median over calls of the call's latest workgroup there; and the
+    timeline of each call's critical workgroup (the one that finished last),
+    median over calls.  Also whether every split of a (sequence, kv head)
+    pair ran on one XCD."""
+    from naivllm_amd import _lib
+    from naivllm_amd.layers.attention import verify_attention_plan
+
+    h = _lib.lib()
+    wgs_max, slots = 4096, 16
+    calls = wl.layers
+    npts = len(STAMP_POINTS)
+    buf = torch.zeros(calls * wgs_max * slots, dtype=torch.int64, device=wl.q.device)
+    rc = h.nsv_stamp_configure(buf.data_ptr(), calls)
+    if rc != 0:
+        raise SystemExit("--stamps needs libnaivspec_stamp.so (python -m naivllm_amd.build --stamp)")
+    for _ in range(2):
+        wl.step(split)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        wl.step(split)
+    every = [[] for _ in range(npts)]
+    latest = [[] for _ in range(npts)]
+    critical = [[] for _ in range(npts)]
+    same_xcd = True
+    kind, splits = verify_attention_plan(wl.B, wl.H, wl.Hkv, wl.D, wl.bs, wl.max_blocks, wl.rows, torch.bfloat16)
+    P8 = (wl.B * wl.Hkv + 7) // 8
+    for _ in range(replays):
+        buf.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        st = buf.view(calls, wgs_max, slots).cpu().numpy()
+        for c in range(calls):
+            used = np.nonzero(st[c, :, 0] > 0)[0]
+            t = st[c][used][:, :npts].astype(np.float64)
+            t0 = t[:, 0].min()
+            rel = np.where(t > 0, (t - t0) * 0.01, np.nan)
+            for i in range(npts):
+                v = rel[:, i]
+                v = v[~np.isnan(v)]
+                if v.size:
+                    every[i].extend(v.tolist())
+                    latest[i].append(float(v.max()))
+            crit = int(np.nanargmax(np.nanmax(rel, axis=1)))
+            for i in range(npts):
+                if not np.isnan(rel[crit, i]):
+                    critical[i].append(float(rel[crit, i]))
+            if kind == "key-split":
+                xcd = st[c, :, slots - 1]
+                groups = {}
+                for wg in used:
+                    pair = ((wg >> 3) % P8) * 8 + (wg & 7)
+                    groups.setdefault(pair, set()).add(int(xcd[wg]))
+                same_xcd &= all(len(v) == 1 for v in groups.values())
+    h.nsv_stamp_configure(None, 0)
+    med = lambda v: round(float(np.median(v)), 2)  # noqa: E731
+    out = {"kernel": kind, "splits": splits, "calls": calls * replays, "points_us": {}, "critical_workgroup_us": {}}
+    for i, name in enumerate(STAMP_POINTS):
+        if every[i]:
+            out["points_us"][name] = {"median": med(every[i]), "latest_per_call": med(latest[i])}
+        if critical[i]:
+            out["critical_workgroup_us"][name] = med(critical[i])
+    out["pair_splits_on_one_xcd"] = bool(same_xcd)
+    return out
+
+
 def rejection_sampling(seed: int = 2, sets: int = 8) -> dict:
     """BASELINE config 2's rejection sampling on the GPU: B = 8, K = 8 model
     drafts per sequence over V = 151936, bf16 draft logits ~ N(0, 2^2) and
@@ -450,6 +526,9 @@ def main():
     ap.add_argument("--no-e2e", action="store_true", help="skip the config-3 end-to-end round measurement")
     ap.add_argument("--no-cascade", action="store_true",
                     help="skip the config-5 measurement (Qwen3-0.6B drafter feeding Qwen3-8B, hybrid, T=1)")
+    ap.add_argument("--stamps", action="store_true",
+                    help="load libnaivspec_stamp.so, print the kernel's per-workgroup timeline of the workload "
+                         "(medians over workgroups, graph-replayed like the metric) and exit")
     ap.add_argument("--seed", type=int, default=2)
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run only a plain device copy of this many MiB (calibrates rocprofv3's "
@@ -462,6 +541,8 @@ def main():
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus})",
               file=sys.stderr)
         raise SystemExit(2)
+    if args.stamps:
+        os.environ["NSV_STAMP_LIB"] = "1"  # read when the library is first loaded
     if not torch.cuda.is_available():
         raise SystemExit("bench.py needs a GPU")
     dev = torch.device("cuda:0")
@@ -473,6 +554,9 @@ def main():
     print(f"[bench] workload: {wl.name}; ctx={wl.ctx}", file=sys.stderr, flush=True)
     if args.ceiling:
         print(json.dumps({"ceiling": ceilings(wl)}), flush=True)
+        return
+    if args.stamps:
+        print(json.dumps({"stamps": stamp_timeline(wl, args.split)}), flush=True)
         return
     # One step (every layer's verify-attention call) is captured as a hipGraph
     # and replayed, as the verify round runs it: the timed region holds GPU

@@ -131,6 +131,16 @@ int nsv_verify_attention_noalloc(void* out, const void* q, const void* k_cache,
                                  int max_blocks, int max_q_len, int dtype,
                                  int kv_split_tokens, void* stream);
 
+/* Timeline stamps of the verify-attention kernels, no reference
+ * counterpart (a measurement aid).  Only a library built with NSV_STAMP=1
+ * (libnaivspec_stamp.so) records them; the default library returns
+ * NSV_ERR_UNSUPPORTED.  `buf` is device memory of calls * 4096 * 16 uint64
+ * words: the i-th launch after this call writes, from thread 0 of each of
+ * its workgroups w < 4096, the 100 MHz s_memrealtime clock at the kernel's
+ * numbered points into words [(i % calls) * 4096 + w] * 16 + point, and the
+ * XCD the workgroup ran on into word 15.  calls = 0 turns stamping off. */
+int nsv_stamp_configure(void* buf, int calls);
+
 /* The kernel nsv_verify_attention runs for these arguments on a device
  * with `cus` compute units (cus <= 0: the current device) and the key
  * splits per sequence it cuts (1: none).  Host-only query, launches

@@ -16,6 +16,9 @@ import torch  # noqa: F401  (must be imported before the library is loaded)
 
 LIB_NAME = "libnaivspec.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+# The same kernels built with timeline stamps (NSV_STAMP=1), loaded instead
+# when NSV_STAMP_LIB=1 is set before the first call (bench.py --stamps).
+STAMP_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libnaivspec_stamp.so")
 
 NSV_F32 = 0
 NSV_BF16 = 1
@@ -30,6 +33,7 @@ SIGNATURES: dict[str, tuple] = {
     "nsv_verify_attention_workspace_size": (
         _c_size, [_c_int] * 9),
     "nsv_verify_attention_plan": (_c_int, [_c_int] * 10 + [_c_vp] * 2),
+    "nsv_stamp_configure": (_c_int, [_c_vp, _c_int]),
     "nsv_verify_attention": (
         _c_int,
         [_c_vp] * 8 + [_c_f32] + [_c_int] * 10 + [_c_vp, _c_size, _c_vp]),
@@ -82,11 +86,12 @@ class NaivspecError(RuntimeError):
 def lib() -> ctypes.CDLL:
     global _lib
     if _lib is None:
-        if not os.path.exists(LIB_PATH):
+        path = STAMP_LIB_PATH if os.environ.get("NSV_STAMP_LIB") == "1" else LIB_PATH
+        if not os.path.exists(path):
             raise RuntimeError(
-                f"{LIB_PATH} is missing: build it with naivllm_amd.build.build_library() "
+                f"{path} is missing: build it with naivllm_amd.build.build_library() "
                 "(or __graft_entry__.build()); there is no non-HIP fallback")
-        handle = ctypes.CDLL(LIB_PATH)
+        handle = ctypes.CDLL(path)
         for name, (res, args) in SIGNATURES.items():
             fn = getattr(handle, name)
             fn.restype = res

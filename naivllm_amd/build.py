@@ -17,6 +17,7 @@ PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
 BUILD_DIR = os.path.join(PKG_DIR, "_build")
 LIB_PATH = os.path.join(PKG_DIR, "libnaivspec.so")
+STAMP_LIB_PATH = os.path.join(PKG_DIR, "libnaivspec_stamp.so")
 
 ARCH = "gfx950"
 HIPCC_FLAGS = [
@@ -41,32 +42,40 @@ def sources() -> list[str]:
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
-def _compile(src: str, hipcc: str) -> str:
-    obj = os.path.join(BUILD_DIR, os.path.basename(src)[:-4] + ".o")
-    cmd = [hipcc, *HIPCC_FLAGS, "-c", src, "-o", obj]
+def _compile(src: str, hipcc: str, build_dir: str, extra: list[str]) -> str:
+    obj = os.path.join(build_dir, os.path.basename(src)[:-4] + ".o")
+    cmd = [hipcc, *HIPCC_FLAGS, *extra, "-c", src, "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{res.stdout}\n{res.stderr}")
     return obj
 
 
-def build_library(verbose: bool = False) -> str:
+def build_library(verbose: bool = False, stamp: bool = False) -> str:
+    """Build libnaivspec.so, or with ``stamp`` its timeline-stamped twin
+    libnaivspec_stamp.so (NSV_STAMP=1: the verify-attention kernels record
+    per-workgroup clock stamps; see nsv_stamp_configure)."""
     hipcc = _hipcc()
-    os.makedirs(BUILD_DIR, exist_ok=True)
+    build_dir = BUILD_DIR + ("_stamp" if stamp else "")
+    out = STAMP_LIB_PATH if stamp else LIB_PATH
+    extra = ["-DNSV_STAMP=1"] if stamp else []
+    os.makedirs(build_dir, exist_ok=True)
     srcs = sources()
     workers = max(1, min(len(srcs), os.cpu_count() or 1, 8))
     with concurrent.futures.ThreadPoolExecutor(workers) as pool:
-        objs = list(pool.map(lambda s: _compile(s, hipcc), srcs))
-    tmp = LIB_PATH + ".tmp"
+        objs = list(pool.map(lambda s: _compile(s, hipcc, build_dir, extra), srcs))
+    tmp = out + ".tmp"
     cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
-        raise RuntimeError(f"link of libnaivspec.so failed:\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, LIB_PATH)
+        raise RuntimeError(f"link of {os.path.basename(out)} failed:\n{res.stdout}\n{res.stderr}")
+    os.replace(tmp, out)
     if verbose:
-        print(f"built {LIB_PATH} from {len(srcs)} sources")
-    return LIB_PATH
+        print(f"built {out} from {len(srcs)} sources")
+    return out
 
 
 if __name__ == "__main__":
-    build_library(verbose=True)
+    import sys
+
+    build_library(verbose=True, stamp="--stamp" in sys.argv[1:])

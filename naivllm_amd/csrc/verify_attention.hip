@@ -76,6 +76,18 @@ constexpr int bf16_stages(int MT, int DH, int DC, bool UPAGE) {
 }
 constexpr float kNegInf = -__builtin_inff();
 
+// Timeline stamps (a build knob: libnaivspec_stamp.so is built with
+// NSV_STAMP=1; the default library has no stamp code).  Thread 0 of every
+// workgroup of a stamped launch writes the 100 MHz constant clock
+// (s_memrealtime, 10 ns ticks, one clock for the whole chip) at numbered
+// points of the kernel into its row of kStampSlots words, and its XCD id
+// into the last word.
+#ifndef NSV_STAMP
+#define NSV_STAMP 0
+#endif
+constexpr int kStampSlots = 16;
+constexpr int kStampMaxWgs = 4096;  // workgroups a stamped launch records
+
 struct VerifyArgs {
   const void* q;
   const void* k_cache;
@@ -95,7 +107,32 @@ struct VerifyArgs {
   int ks_splits;     // key-split kernel: splits per sequence when split_tokens == 0
   int m_base;        // fp32 kernel: first query row (of the Mv) this launch serves
   int dmerge;        // d-sliced kernel: the pair's last workgroup merges its splits in-kernel (else a merge launch)
+#if NSV_STAMP
+  unsigned long long* stamps;  // [grid][kStampSlots] of this launch, or null
+#endif
 };
+
+#if NSV_STAMP
+#define NSV_STAMP_AT(a, slot)                                                                      \
+  do {                                                                                             \
+    if ((a).stamps && threadIdx.x == 0)                                                            \
+      (a).stamps[blockIdx.x * kStampSlots + (slot)] = __builtin_amdgcn_s_memrealtime();            \
+  } while (0)
+// hwreg(HW_REG_XCC_ID = 20, offset 0, 4 bits): the XCD the workgroup runs on
+#define NSV_STAMP_XCC(a)                                                                           \
+  do {                                                                                             \
+    if ((a).stamps && threadIdx.x == 0)                                                            \
+      (a).stamps[blockIdx.x * kStampSlots + kStampSlots - 1] =                                     \
+          (unsigned long long)(__builtin_amdgcn_s_getreg(20 | (3 << 11)) & 15);                    \
+  } while (0)
+#else
+#define NSV_STAMP_AT(a, slot) \
+  do {                        \
+  } while (0)
+#define NSV_STAMP_XCC(a) \
+  do {                   \
+  } while (0)
+#endif
 
 __device__ __forceinline__ u32x4 load16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 
@@ -843,6 +880,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
   const int wg = blockIdx.x;
   const int yy = wg >> 3;
   fetch_args(a);
+  NSV_STAMP_AT(a, 0);  // entry
+  NSV_STAMP_XCC(a);
   const int pair_raw = (yy % a.P8) * 8 + (wg & 7);
   const int split = yy / a.P8;
   // (the grid rounds the pair count up to a multiple of 8: workgroups past
@@ -947,6 +986,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
   uint16_t* vl = reinterpret_cast<uint16_t*>(smem) + w * TK * VSTR;
   unsigned char* kl = smem + NW * TK * VSTR * 2 + (WROW ? w * TK * DH * 2 : 0);
   __syncthreads();  // block-table row visible
+  NSV_STAMP_AT(a, 1);  // metadata back
 
   const int ntiles = (ke - kb + TK - 1) / TK;
   const int niter = (ntiles + NW - 1) / NW;  // same trip count in every wave
@@ -1099,6 +1139,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
     for (int it = 0; it < niter; it += 2) {
       __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): tile it landed
       __builtin_amdgcn_sched_barrier(0);
+      if (it == 0) NSV_STAMP_AT(a, 2);  // first tile landed
       if (it + 1 < niter) issue(T1, it + 1);
       __builtin_amdgcn_sched_barrier(0);
       compute(T0);
@@ -1132,6 +1173,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
     }
   }
 
+  NSV_STAMP_AT(a, 3);  // key loop done (wave 0)
+
   // ---- merge the waves' (max, sum, O) ---------------------------------------
   if (g4 == 0) {
 #pragma unroll
@@ -1141,6 +1184,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
     }
   }
   __syncthreads();  // also: every wave is done with its staging rows
+  NSV_STAMP_AT(a, 7);  // every wave's key loop done
   // every lane: the split's max over the waves for its rows, and its own
   // waves' rescale factor; wave 0 keeps the split's (max, sum) per row
   // (every LDS read of a step is issued before the first is used: the
@@ -1198,6 +1242,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
       }
     }
     __syncthreads();
+    if (ps == 0) NSV_STAMP_AT(a, 8);  // O rows in LDS
     f32x4 wv[ITEMS][NW];
 #pragma unroll
     for (int j = 0; j < ITEMS; ++j) {
@@ -1232,6 +1277,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
       }
     }
   }
+  NSV_STAMP_AT(a, 4);  // waves merged, partials issued
   if (nsplit == 1) return;
   // the split's (max, sum) per row, written by wave 0 before the barrier above
   // (stored only now, so that barrier did not wait for the store's acknowledgement)
@@ -1285,6 +1331,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
     is_last = __hip_atomic_fetch_add(&a.counters[counter_slot(pair)], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
               (unsigned)(nsplit - 1);
   __syncthreads();
+  NSV_STAMP_AT(a, 5);  // arrival counted
   if (!uniform(is_last)) return;
   if (tid == 0) __hip_atomic_store(&a.counters[counter_slot(pair)], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   const int64_t base0 = (int64_t)pair * a.S * a.Mv;  // row 0 of split 0
@@ -1372,10 +1419,12 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
   };
   if (nsplit <= 4) {
     merge_in_one_trip(std::integral_constant<int, 4>{});
+    NSV_STAMP_AT(a, 6);  // merge stores issued (last split)
     return;
   }
   if (nsplit <= 8) {
     merge_in_one_trip(std::integral_constant<int, 8>{});
+    NSV_STAMP_AT(a, 6);
     return;
   }
   // more splits: CH per round trip
@@ -2051,11 +2100,31 @@ int launch_verify(const VerifyArgs& a, const Plan& p, int D, int dtype, hipStrea
 }
 
 
+#if NSV_STAMP
+unsigned long long* g_stamp_buf = nullptr;  // [calls][kStampMaxWgs][kStampSlots]
+int g_stamp_calls = 0;
+unsigned g_stamp_next = 0;
+#endif
+
 }  // namespace
 
 extern "C" {
 
 int nsv_version(void) { return 100; }
+
+int nsv_stamp_configure(void* buf, int calls) {
+#if NSV_STAMP
+  if (calls < 0 || (calls > 0 && !buf)) return NSV_ERR_ARG;
+  g_stamp_buf = calls > 0 ? (unsigned long long*)buf : nullptr;
+  g_stamp_calls = calls;
+  g_stamp_next = 0;
+  return NSV_OK;
+#else
+  (void)buf;
+  (void)calls;
+  return NSV_ERR_UNSUPPORTED;
+#endif
+}
 
 const char* nsv_error_string(int code) {
   switch (code) {
@@ -2140,6 +2209,11 @@ int nsv_verify_attention(void* out, const void* q, const void* k_cache, const vo
   // one launch (and merge) per subset of each kv head's query heads; they
   // share the workspace in stream order
   for (a.g0 = 0; a.g0 < p.Gs; a.g0 += p.G) {
+#if NSV_STAMP
+    a.stamps = nullptr;
+    if (g_stamp_buf && 8 * p.S * a.P8 * p.dqc <= kStampMaxWgs)
+      a.stamps = g_stamp_buf + (size_t)(g_stamp_next++ % (unsigned)g_stamp_calls) * kStampMaxWgs * kStampSlots;
+#endif
     rc = launch_verify(a, p, D, dtype, s);
     if (rc != NSV_OK) return rc;
   }
