@@ -104,16 +104,18 @@ class Workload:
             self.call(layer, split)
 
 
-TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "verify_attn_config2_traffic.md")
+def traffic_profile(workload_config: int) -> str:
+    return os.path.join(ROOT, "profiles", f"verify_attn_config{workload_config}_traffic.md")
 
 
 def measured_traffic(workload_config: int):
     """HBM bytes per verify-attention launch from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE passes (copy-calibrated), for the config-2
-    workload those passes ran; None otherwise."""
-    if workload_config != 2 or not os.path.exists(TRAFFIC_PROFILE):
+    FETCH_SIZE / WRITE_SIZE passes (copy-calibrated) of that workload, or
+    None when no such profile is committed."""
+    path = traffic_profile(workload_config)
+    if not os.path.exists(path):
         return None
-    for line in open(TRAFFIC_PROFILE):
+    for line in open(path):
         if line.startswith("traffic_bytes:"):
             return int(line.split(":")[1])
     return None
@@ -160,6 +162,59 @@ def e2e_round(batches=(1, 2, 4, 8), tokens: int = 48, K: int = 8) -> dict:
             "output_tokens": m["output_tokens"],
         }
         print(f"[bench] e2e b{b}: {out[f'b{b}']}", file=sys.stderr, flush=True)
+        eng.exit()
+        del eng
+        torch.cuda.empty_cache()
+    return out
+
+
+def e2e_self_draft(batches=(1, 8), tokens: int = 55, K: int = 8) -> dict:
+    """The K=8 regime with every draft accepted.  Random-init Qwen3-0.6B
+    decodes greedily into one repeated token, and for a constant run the
+    n-gram lookup (the reference's rfind from the most recent match) can
+    only ever continue with one token, so n-gram rounds carry at most one
+    draft.  Here the model drafter runs the target's own weights (same
+    seed): its greedy drafts are the target's greedy tokens, so each round
+    verifies and commits K drafts plus the bonus token through the same
+    captured round (K GPU-resident draft steps, one 9-row verify forward,
+    greedy acceptance, commit).  Config-3 prompts, b1 and b8, each batch on
+    a fresh engine after a warm-up request; 55 output tokens (the prefill's
+    first token and 6 whole rounds of K + 1), so no round is cut short by
+    max_tokens.  Acceptance = accepted drafts / drafted, an accepted draft
+    being a committed token other than each sequence's per-round bonus or
+    correction token."""
+    from naivllm_amd.layers.qwen3 import Qwen3Config
+    from naivllm_amd.sampling_parameters import SamplingParams
+    from naivllm_amd.spec_engine.spec_llm_engine import SpecLLMEngine
+
+    sp = SamplingParams(temperature=0.0, max_tokens=tokens, ignore_eos=True)
+    out = {"drafter": "model drafter with the target's own weights (Qwen3-0.6B, same seed): self-speculation"}
+    for b in batches:
+        eng = SpecLLMEngine(dict(spec_method="model", num_speculative_tokens=K, model_config=Qwen3Config.qwen3_0_6b(),
+                                 draft_model_config=Qwen3Config.qwen3_0_6b(), draft_seed=0, seed=0,
+                                 max_num_sequences=max(batches), max_model_length=1200 + 16 + tokens + 64,
+                                 block_size=256))
+        eng.generate(synth.config3_prompts(1, seed=99), SamplingParams(temperature=0.0, max_tokens=4,
+                                                                        ignore_eos=True))  # graphs captured, warm
+        before = dict(eng.spec_stats)
+        res = eng.generate(synth.config3_prompts(b), sp)
+        m = res["metrics"]
+        st = m["spec_decoding"]
+        drafted = st["drafted_tokens"] - before["drafted_tokens"]
+        accepted = st["accepted_tokens"] - before["accepted_tokens"]
+        rounds = max(m["rounds"], 1)
+        out[f"b{b}"] = {
+            "decode_tok_s": round(m["decode_tok_per_s"], 1),
+            "output_tok_s": round(m["output_tok_per_s"], 1),
+            "decode_ms_per_round": round(1e3 * m["decode_s"] / rounds, 3),
+            "rounds": m["rounds"],
+            "tokens_per_round": round(m["decode_tokens"] / rounds, 3),
+            "drafted": drafted,
+            "committed": accepted,
+            "acceptance": round((accepted - m["rounds"] * b) / max(drafted, 1), 4) if drafted else None,
+            "output_tokens": m["output_tokens"],
+        }
+        print(f"[bench] self-draft b{b}: {out[f'b{b}']}", file=sys.stderr, flush=True)
         eng.exit()
         del eng
         torch.cuda.empty_cache()
@@ -436,6 +491,29 @@ def stamp_timeline(wl: "Workload", split: int, replays: int = 10) -> dict:
     return out
 
 
+def config4_line(seed: int, steps: int = 20) -> dict:
+    """BASELINE config 4 beside the metric's workload: verify attention at the
+    Qwen3-8B layer shape (B=16, 32Q/8KV heads, d=128, bf16, 256-token pages,
+    contexts uniform in [16k, 32k], K=8), the two rotating pools of
+    1,700 pages (1.8 GB each, K and V) far past the Infinity Cache; timed like
+    the metric (a hipGraph of one call per pool, HIP events around the
+    replays), with its own load-only floor and stream ceilings."""
+    wl = Workload(4, 2, seed, torch.device("cuda:0"))
+    us = _graph_us(lambda: wl.step(0), wl.layers, steps=steps)
+    gbs = wl.bytes / us / 1e3
+    tflops = wl.flops / us / 1e6
+    out = {"workload": wl.name, "context_lens_sum": int(sum(wl.ctx)), "us_per_call": round(us, 3),
+           "bytes_per_call": wl.bytes, "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4),
+           "mfma_tflops": round(tflops, 2), "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 5),
+           "traffic": measured_traffic(4), "ceiling": ceilings(wl)}
+    c = out["ceiling"]
+    c["kernel_vs_load_floor"] = round(c["load_floor_us"] / us, 4)
+    c["kernel_vs_stream"] = round(c["stream_us"] / us, 4)
+    del wl
+    torch.cuda.empty_cache()
+    return out
+
+
 def rejection_sampling(seed: int = 2, sets: int = 8) -> dict:
     """BASELINE config 2's rejection sampling on the GPU: B = 8, K = 8 model
     drafts per sequence over V = 151936, bf16 draft logits ~ N(0, 2^2) and
@@ -591,9 +669,13 @@ def main():
     print(f"[bench] ceilings: {ceil}", file=sys.stderr, flush=True)
     wl.k_caches, wl.v_caches = [], []  # free the pools before the other measurements
     torch.cuda.empty_cache()
+    c4 = None if args.config == 4 else config4_line(args.seed)
+    if c4 is not None:
+        print(f"[bench] config 4: {c4}", file=sys.stderr, flush=True)
     accept = rejection_sampling()
     print(f"[bench] acceptance: {accept}", file=sys.stderr, flush=True)
     e2e = None if args.no_e2e else e2e_round()
+    self_draft = None if args.no_e2e else e2e_self_draft()
     cascade = None if (args.no_e2e or args.no_cascade) else e2e_cascade()
     cpu = None if args.no_cpu else cpu_baseline()
     line = {
@@ -616,13 +698,16 @@ def main():
         "us_per_call": round(us_per_call, 3),
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(args.config),
-                     "traffic_source": "profiles/verify_attn_config2_traffic.md (rocprofv3 FETCH_SIZE x2 + WRITE_SIZE x1)",
+                     "traffic_source": f"profiles/verify_attn_config{args.config}_traffic.md (rocprofv3 FETCH_SIZE "
+                                       f"x2 + WRITE_SIZE x1)",
                      "bytes_per_call": wl.bytes, "mfma_tflops": round(tflops, 2),
                      "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 5)},
         "ceiling": dict(ceil, kernel_vs_load_floor=round(ceil["load_floor_us"] / us_per_call, 4),
                         kernel_vs_stream=round(ceil["stream_us"] / us_per_call, 4)),
+        "config4": c4,
         "rejection_sampling": accept,
         "accepted_tok_s": e2e,
+        "accepted_tok_s_k8_self_draft": self_draft,
         "cascade_tok_s": cascade,
         "cpu_baseline": cpu,
     }

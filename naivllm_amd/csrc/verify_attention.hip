@@ -50,12 +50,6 @@ constexpr int kMaxCounterPairs = 16384;
 // (device-scope atomics on one line serialise, ~20 ns apiece), and pair
 // p + 256 k shares p's line.
 __device__ __forceinline__ int counter_slot(int pair) { return ((pair & 255) << 6) | (pair >> 8); }
-#ifndef NSV_KS_SHORT_TILES
-#define NSV_KS_SHORT_TILES 4  // key-split splits of at most this many tiles per wave keep one tile in flight
-#endif
-#ifndef NSV_MAX_STAGES
-#define NSV_MAX_STAGES 4  // deepest key-split pipeline
-#endif
 
 
 // Pipeline depth of the d-sliced bf16 kernel.  Its slices re-read the pair's
@@ -833,7 +827,7 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
 //                 (g4, c) element i = key 4 g4 + i, query row c) is already
 //                 the B operand P^T; V^T comes from the wave's LDS copy of
 //                 the tile through one transposing read per 16 dims.
-// An NS-stage register pipeline keeps the next NS tiles' loads in flight.
+// Each wave keeps one tile in flight: the next is issued when one lands.
 // The sequence's whole block-table row is fetched in the first round trip
 // (with the context length and query range), so no load waits on another.
 #ifndef NSV_KS_WROW
@@ -844,7 +838,7 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
 // at slot X ^ (r % VCH)) into the operand layout; a CU ingests whole rows
 // several times faster than the operand order's 64 bytes from each of 16
 // keys (config 4 on MI355X: 369 -> 356 us per call).
-template <int MT, int DH, int NS, int NW, bool WROW = (NSV_KS_WROW != 0)>
+template <int MT, int DH, int NW, bool WROW = (NSV_KS_WROW != 0)>
 __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyArgs a) {
   constexpr int NT = NW * 64;
   constexpr int TK = 16;          // keys per wave tile
@@ -1120,57 +1114,34 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
     __builtin_amdgcn_wave_barrier();
   };
 
-  // ---- pipeline over this wave's tiles
+  // ---- pipeline over this wave's tiles: one tile in flight per wave, the
+  // next issued as soon as the current one has landed and before it is
+  // computed, so the arithmetic hides under the next tile's flight.  More
+  // tiles in flight only queue more requests and lower the memory system's
+  // rate for this access pattern (MI355X, graph-replayed: config 2 15.6 us
+  // with one, 17.8 with two, 18.2 with every tile of the wave at once;
+  // config 4 328.6 us with one against 337.3 with a two-stage pipeline).
   load_q();
-  if constexpr (NS == 1) {
-    // Short splits (a few tiles per wave): at most one tile in flight per
-    // wave, and the next tile is issued as soon as the current one has
-    // landed, before it is computed, so the arithmetic hides under the next
-    // tile's flight.  (More tiles in flight only queue more requests at the
-    // same bandwidth: on MI355X at config 2 the loads alone take 9.2 us
-    // with one tile per wave in flight, 9.6 with two, 10.3 with four.)
-    Tile T0, T1;
+  Tile T0, T1;
+  __builtin_amdgcn_sched_barrier(0);
+  issue(T0, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  finish_positions();
+  store_q();
+  lds_barrier();  // query rows visible; the first tile stays in flight
+  for (int it = 0; it < niter; it += 2) {
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): tile it landed
     __builtin_amdgcn_sched_barrier(0);
-    issue(T0, 0);
+    if (it == 0) NSV_STAMP_AT(a, 2);  // first tile landed
+    if (it + 1 < niter) issue(T1, it + 1);
     __builtin_amdgcn_sched_barrier(0);
-    finish_positions();
-    store_q();
-    lds_barrier();  // query rows visible; the first tile stays in flight
-    for (int it = 0; it < niter; it += 2) {
-      __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): tile it landed
-      __builtin_amdgcn_sched_barrier(0);
-      if (it == 0) NSV_STAMP_AT(a, 2);  // first tile landed
-      if (it + 1 < niter) issue(T1, it + 1);
-      __builtin_amdgcn_sched_barrier(0);
-      compute(T0);
-      if (it + 1 >= niter) break;
-      __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): tile it + 1 landed
-      __builtin_amdgcn_sched_barrier(0);
-      if (it + 2 < niter) issue(T0, it + 2);
-      __builtin_amdgcn_sched_barrier(0);
-      compute(T1);
-    }
-  } else {
-    // Long splits: an NS-stage register pipeline (the next NS tiles in
-    // flight while one computes).  Every issue is unconditional (tiles past
-    // the split read a mapped row), which keeps the compiler's wait counts
-    // exact across iterations.
-    Tile T[NS];
+    compute(T0);
+    if (it + 1 >= niter) break;
+    __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): tile it + 1 landed
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int s = 0; s < NS; ++s) issue(T[s], s);
+    if (it + 2 < niter) issue(T0, it + 2);
     __builtin_amdgcn_sched_barrier(0);
-    finish_positions();
-    store_q();
-    lds_barrier();  // query rows visible; the tile loads stay in flight
-    for (int it = 0; it < niter; it += NS) {
-#pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        __builtin_amdgcn_sched_barrier(0);
-        compute(T[s]);
-        issue(T[s], it + s + NS);
-      }
-    }
+    compute(T1);
   }
 
   NSV_STAMP_AT(a, 3);  // key loop done (wave 0)
@@ -1711,7 +1682,6 @@ struct Plan {
   int Gs;         // query heads per kv head; launches serve G of them at a time (Gs / G launches)
   int ks;         // 1: key-split kernel, 0: d-sliced kernel (bf16)
   int ks_splits;  // key-split kernel, automatic splits per sequence (split == 0)
-  int ks_short;   // key-split kernel: at most 4 tiles per wave, one tile in flight per wave
 };
 
 int ilog2_exact(int v) {
@@ -1765,7 +1735,6 @@ int make_plan(int B, int H, int Hkv, int D, int block_size, int max_blocks, int 
   p->dqc = 1;
   p->ks = 0;
   p->ks_splits = 0;
-  p->ks_short = 0;
   // Kernel choice (bf16).  The key-split kernel reads every K/V byte once
   // per CU but pays about three memory round trips to merge a pair's splits;
   // the d-sliced kernel needs no cross-workgroup merge but re-reads the
@@ -1808,9 +1777,6 @@ int make_plan(int B, int H, int Hkv, int D, int block_size, int max_blocks, int 
       p->S = (int)((max_ctx + split - 1) / split);
     }
     if (p->S > 8192) return NSV_ERR_UNSUPPORTED;  // the merge stages 2 * S floats in LDS
-    // keys one split covers at most, and the 16-key tiles each of the 8 waves takes
-    const int64_t split_keys = p->split > 0 ? p->split : (max_ctx + p->S - 1) / p->S;
-    p->ks_short = (split_keys + 16 * kKsWaves - 1) / (16 * kKsWaves) <= NSV_KS_SHORT_TILES;
     return NSV_OK;
   }
   if (dtype == NSV_BF16) {
@@ -1863,38 +1829,14 @@ void launch_bf16_dc(const VerifyArgs& a, dim3 grid, hipStream_t s) {
     hipLaunchKernelGGL((verify_attn_bf16_kernel<MT, DH, DC, false, bf16_stages(MT, DH, DC, false)>), grid, dim3(kBf16Waves * 64), 0, s, a);
 }
 
-// Pipeline depth of the key-split kernel: as many K/V tiles in flight per
-// wave as the 256 VGPRs of a two-waves-per-SIMD launch hold without
-// spilling.  The estimate (VGPRs = 20 + MT * (per query m-tile) + NS * (per
-// tile)) still counts 4 KS VGPRs per m-tile for the query operand, which now
-// lives in LDS: that share is headroom (no instantiation spills), and the
-// third stage it would buy at three m-tiles measured slower on MI355X
-// (config 4: 332 vs 325 us per call).
-constexpr int ks_stages(int MT, int DH) {
-  const int KS = DH / 32, DT = DH / 16, VL = 16 / (64 / (DH / 8));
-  const int fixed = 20 + MT * (KS * 4 + DT * 4 + 8);
-  const int ns = (256 - fixed) / (4 * KS + 4 * VL);
-  return ns < 2 ? 2 : (ns > NSV_MAX_STAGES ? NSV_MAX_STAGES : ns);
-}
-
 template <int MT>
-int launch_ks(const VerifyArgs& a, int D, bool short_splits, dim3 grid, hipStream_t s) {
+int launch_ks(const VerifyArgs& a, int D, dim3 grid, hipStream_t s) {
   if constexpr (MT <= 3) {
     constexpr int NW = kKsWaves;
-    if (short_splits) {
-      // few tiles per wave: one in flight per wave (a deeper pipeline only
-      // queues more requests at the same bandwidth; measured on MI355X at
-      // config 2: 1 stage 9.2 us, 2 stages 9.6, 4 stages 10.3 for the loads alone)
-      if (D == 128)
-        hipLaunchKernelGGL((verify_attn_ks_kernel<MT, 128, 1, NW>), grid, dim3(NW * 64), 0, s, a);
-      else
-        hipLaunchKernelGGL((verify_attn_ks_kernel<MT, 64, 1, NW>), grid, dim3(NW * 64), 0, s, a);
-      return NSV_OK;
-    }
     if (D == 128)
-      hipLaunchKernelGGL((verify_attn_ks_kernel<MT, 128, ks_stages(MT, 128), NW>), grid, dim3(NW * 64), 0, s, a);
+      hipLaunchKernelGGL((verify_attn_ks_kernel<MT, 128, NW>), grid, dim3(NW * 64), 0, s, a);
     else
-      hipLaunchKernelGGL((verify_attn_ks_kernel<MT, 64, ks_stages(MT, 64), NW>), grid, dim3(NW * 64), 0, s, a);
+      hipLaunchKernelGGL((verify_attn_ks_kernel<MT, 64, NW>), grid, dim3(NW * 64), 0, s, a);
     return NSV_OK;
   }
   return NSV_ERR_UNSUPPORTED;
@@ -2065,9 +2007,9 @@ int launch_verify(const VerifyArgs& a, const Plan& p, int D, int dtype, hipStrea
   const dim3 grid(8 * p.S * a.P8 * p.dqc);
   if (dtype == NSV_BF16 && p.ks) {
     switch (p.MT) {
-      case 1: rc = launch_ks<1>(a, D, p.ks_short, grid, s); break;
-      case 2: rc = launch_ks<2>(a, D, p.ks_short, grid, s); break;
-      default: rc = launch_ks<3>(a, D, p.ks_short, grid, s); break;
+      case 1: rc = launch_ks<1>(a, D, grid, s); break;
+      case 2: rc = launch_ks<2>(a, D, grid, s); break;
+      default: rc = launch_ks<3>(a, D, grid, s); break;
     }
     if (rc != NSV_OK) return rc;
   } else if (dtype == NSV_BF16) {
