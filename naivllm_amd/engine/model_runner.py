@@ -23,6 +23,7 @@ from __future__ import annotations
 import torch
 
 from naivllm_amd.layers.qwen3 import Qwen3Verify
+from naivllm_amd.utils.context import get_context, reset_context, set_context
 
 BUCKETS = (1, 2, 4, 8, 16, 32)
 
@@ -69,23 +70,30 @@ class ModelRunner:
                 [table[p // self.block_size] * self.block_size + p % self.block_size for p in pos])
 
     # ------------------------------------------------------------------ eager
-    def prepare_spec_verify(self, seqs):
-        """Packed rows of ``seqs`` (model_runner.py:443-483): returns
-        (input_ids, positions, slot_mapping, block_tables, context_lens,
-        cu_seqlens_q, max_q_len) on the model's device."""
-        ids, pos, slots, cu = [], [], [], [0]
+    def prepare_spec_verify(self, seqs) -> torch.Tensor:
+        """Packed rows of ``seqs`` (model_runner.py:443-483): publishes the
+        step's metadata with ``set_context`` (is_prefill and is_verify set,
+        cu_seqlens_q, max_seqlen_q/k, slot_mapping, context_lens,
+        block_tables -1 padded, seqlens_q/k, positions) for the layers to
+        read, and returns the rows' input_ids, all on the model's device."""
+        ids, pos, slots, cu, qlens = [], [], [], [0], []
         for seq in seqs:
             a, b, c = self._rows(seq)
             ids += a
             pos += b
             slots += c
             cu.append(cu[-1] + len(a))
+            qlens.append(len(a))
         width = max(len(self._table(s)) for s in seqs)
         bt = [self._table(s) + [-1] * (width - len(self._table(s))) for s in seqs]
+        klens = [len(s) for s in seqs]
         dev = self.model.device
         t = lambda x, dt: torch.tensor(x, dtype=dt, device=dev)  # noqa: E731
-        return (t(ids, torch.int64), t(pos, torch.int64), t(slots, torch.int64), t(bt, torch.int32),
-                t([len(s) for s in seqs], torch.int64), t(cu, torch.int32), max(len(s.draft_tokens) for s in seqs) + 1)
+        set_context(True, is_verify=True, cu_seqlens_q=t(cu, torch.int32), cu_seqlens_k=None,
+                    max_seqlen_q=max(qlens), max_seqlen_k=max(klens), slot_mapping=t(slots, torch.int64),
+                    context_lens=t(klens, torch.int64), block_tables=t(bt, torch.int32), seqlens_q=qlens,
+                    seqlens_k=klens, positions=t(pos, torch.int64))
+        return t(ids, torch.int64)
 
     # ---------------------------------------------------------------- graphed
     def _forward_bucket(self, B: int) -> None:
@@ -121,8 +129,13 @@ class ModelRunner:
         if not seqs:
             raise ValueError("no sequences to verify")
         if not self.verify_graphs:
-            ids, pos, slots, bt, ctx, cu, mq = self.prepare_spec_verify(seqs)
-            return self.model.forward(ids, pos, slots, bt, ctx, cu, mq)
+            ids = self.prepare_spec_verify(seqs)
+            c = get_context()
+            try:
+                return self.model.forward(ids, c.positions, c.slot_mapping, c.block_tables, c.context_lens,
+                                          c.cu_seqlens_q, c.max_seqlen_q)
+            finally:
+                reset_context()
         v = self.verify_vars
         k = v["k"]
         if len(seqs) > self.max_num_sequences:

@@ -183,18 +183,72 @@ def store_kvcache(
     _lib.check(rc, "store_kvcache")
 
 
+_prefill_plan: tuple = (None, None)  # (the Context it was built for, its tensors)
+
+
+def _prefill_rows(ctx, num_heads: int, num_kv_heads: int, device) -> tuple:
+    """Verify-kernel metadata of a prefill step, built once per Context.
+
+    Sequence i has seqlens_q[i] new rows at positions seqlens_k[i] -
+    seqlens_q[i] .. seqlens_k[i] - 1.  Its rows are cut into causal blocks of
+    q_block = 64 // G rows (G query heads per kv head: the kernel holds up to
+    64 query rows per (sequence, kv head)); each block is one entry of the
+    kernel's batch with context = the block's last position + 1, so every
+    row attends exactly keys 0 .. its position.  Block-table row of block j:
+    the sequence's row of context.block_tables (paged prefill) or, without
+    block tables, the sequence's keys in the step's own contiguous K/V read
+    as one-token pages (cu_seqlens_k[i] + p for position p).
+    Returns (block_tables, context_lens, cu_seqlens_q, positions, q_block)."""
+    import numpy as np
+
+    global _prefill_plan
+    if _prefill_plan[0] is ctx:
+        return _prefill_plan[1]
+    if ctx.seqlens_q is None or ctx.seqlens_k is None:
+        raise ValueError("a prefill step needs context.seqlens_q and context.seqlens_k")
+    q_block = max(1, 64 // (num_heads // num_kv_heads))
+    paged = ctx.block_tables is not None
+    tables = ctx.block_tables.cpu().numpy() if paged else None
+    width = tables.shape[1] if paged else max(ctx.seqlens_k)
+    bt, lens, cu, pos = [], [], [0], []
+    k_start = 0
+    for i, (ql, kl) in enumerate(zip(ctx.seqlens_q, ctx.seqlens_k)):
+        if not 0 < ql <= kl:
+            raise ValueError(f"prefill sequence {i}: {ql} query rows over {kl} keys")
+        if paged:
+            row = tables[i].astype(np.int32)
+        else:
+            row = np.full(width, -1, dtype=np.int32)
+            row[:kl] = np.arange(k_start, k_start + kl, dtype=np.int32)
+        for b0 in range(kl - ql, kl, q_block):
+            b1 = min(kl, b0 + q_block)
+            bt.append(row)
+            lens.append(b1)
+            cu.append(cu[-1] + (b1 - b0))
+        pos.append(np.arange(kl - ql, kl, dtype=np.int64))
+        k_start += kl
+    t = lambda x, dt: torch.from_numpy(np.ascontiguousarray(x, dtype=dt)).to(device)  # noqa: E731
+    out = (t(np.stack(bt), np.int32), t(lens, np.int64), t(cu, np.int32), t(np.concatenate(pos), np.int64), q_block)
+    _prefill_plan = (ctx, out)
+    return out
+
+
 class Attention(nn.Module):
     """Attention layer of the reference (layers/attention.py:670-767):
     writes this step's K/V into the paged cache at context.slot_mapping,
     then attends from the query rows the global Context describes:
       * verify (context.is_verify): a chunk of drafted tokens per sequence
         with a causal mask from absolute positions (:704-731);
+      * prefill (context.is_prefill, :733-757): every new prompt row of each
+        sequence, causally over its keys.  With context.block_tables (a
+        prompt behind a cached prefix) the keys come from the paged cache,
+        the step's own K/V already stored in it, as the reference's
+        paged_attention_prefill (:328-363); without, from the step's
+        contiguous K/V, as its varlen flash path (:257-325).  Both run on the
+        verify kernel over causal blocks of rows (``_prefill_rows``);
       * decode (neither flag): one query row per sequence attending its
         whole context (:759-767), served by the same verify kernel with
-        each row at position context_lens - 1.
-    Prefill (context.is_prefill) is not a mode of this class: the verify
-    forward (naivllm_amd.layers.qwen3) prefills prompts through its own
-    chunked path."""
+        each row at position context_lens - 1."""
 
     def __init__(self, num_heads: int, head_dim: int, scale: float = 1.0, num_kv_heads: int | None = None,
                  block_size: int = 16):
@@ -213,11 +267,21 @@ class Attention(nn.Module):
             store_kvcache(k.reshape(-1, self.num_kv_heads, self.head_dim),
                           v.reshape(-1, self.num_kv_heads, self.head_dim),
                           k_cache, v_cache, context.slot_mapping, self.block_size)
-        if context.is_prefill and not context.is_verify:
-            raise ValueError("naivllm_amd.Attention serves verify and decode steps; prefill runs through the "
-                             "verify forward's chunked path")
         scale = self.scale / (self.head_dim ** 0.5)
         q = q.reshape(-1, self.num_heads, self.head_dim)
+        if context.is_prefill and not context.is_verify:
+            if context.cu_seqlens_q is None:
+                raise ValueError("cu_seqlens_q must be provided for varlen attention")
+            bt, lens, cu, positions, q_block = _prefill_rows(context, self.num_heads, self.num_kv_heads, q.device)
+            if context.block_tables is not None:
+                kc, vc, bs = k_cache, v_cache, self.block_size
+            else:  # the step's own keys, one token per page
+                kc = k.reshape(-1, 1, self.num_kv_heads, self.head_dim).contiguous()
+                vc = v.reshape(-1, 1, self.num_kv_heads, self.head_dim).contiguous()
+                bs = 1
+            o = paged_attention_verify(q, kc, vc, bt, lens, cu, positions, scale, self.num_heads, self.num_kv_heads,
+                                       self.head_dim, bs, max(16, q_block), max_q_len=q_block)
+            return o.reshape(o.shape[0], self.num_heads * self.head_dim)
         if context.is_verify:
             max_q_len = max(context.seqlens_q)
             cu, positions = context.cu_seqlens_q, context.positions

@@ -96,15 +96,30 @@ class NgramDrafter:
 class DraftRunner:
     """A draft model with its own paged KV pool, addressed through
     ``seq.draft_block_table`` (the reference's draft ModelRunner,
-    spec_llm_engine.py:104-137, model_runner.py:784-847).  Eager: the
-    device round (engine/verify_round.py) is the graph-captured form."""
+    spec_llm_engine.py:104-137, model_runner.py:784-847).
 
-    def __init__(self, model, num_blocks: int, block_size: int, table_attr: str = "draft_block_table"):
+    ``run_draft_steps`` is the reference's GPU-resident draft loop
+    (``run_draft_steps_gpu``): K decode steps whose sampled tokens feed the
+    next step on the device, one host synchronisation per call.  With
+    ``use_graphs`` the whole K-step loop (both forwards' kernels and the
+    samplers) is captured once per batch bucket {1, 2, 4, ...} and replayed
+    from static buffers the host fills each call, as the reference replays
+    its decode graph K times from static buffers (model_runner.py:784-847);
+    padded rows of a bucket (position -1, slot -1, context 0, table -1) are
+    inert.  A call with a caller-supplied generator at a temperature above
+    1e-6 runs eagerly, so its draws come from that generator (a captured
+    graph draws from torch's device generator)."""
+
+    def __init__(self, model, num_blocks: int, block_size: int, table_attr: str = "draft_block_table",
+                 use_graphs: bool = True):
         model.allocate_kv_cache(num_blocks, block_size)
         self.model = model
         self.block_size = block_size
         self.table_attr = table_attr
         self.device = model.device
+        self.use_graphs = use_graphs
+        self._bufs: dict | None = None
+        self._graphs: dict = {}  # (bucket, stochastic) -> captured graph
 
     def _table(self, seqs) -> torch.Tensor:
         tables = [getattr(s, self.table_attr) for s in seqs]
@@ -123,21 +138,62 @@ class DraftRunner:
             out.append(-1 if p < 0 else table[p // bs] * bs + p % bs)
         return out
 
-    def prefill(self, seqs, chunk: int = 32) -> None:
-        """KV of every token but the last of each sequence (the first draft
-        step feeds the last one), in chunks of ``chunk`` rows."""
-        dev = self.device
-        for s in seqs:
-            table = self._table([s])
-            n = len(s.token_ids) - 1
-            for p0 in range(0, n, chunk):
-                p1 = min(n, p0 + chunk)
-                pos = list(range(p0, p1))
-                ids = torch.tensor(s.token_ids[p0:p1], dtype=torch.int64, device=dev)
-                self.model.forward(ids, torch.tensor(pos, dtype=torch.int64, device=dev),
-                                   torch.tensor(self._slots([s] * len(pos), pos), dtype=torch.int64, device=dev),
-                                   table, torch.tensor([p1], dtype=torch.int64, device=dev),
-                                   torch.tensor([0, p1 - p0], dtype=torch.int32, device=dev), p1 - p0)
+    def prefill(self, seqs, starts=None) -> None:
+        """KV of the tokens of each sequence from ``starts[i]`` (default 0: the
+        draft pool's own prefix is empty) in one forward over every sequence
+        (Qwen3Verify.prefill: causal blocks through the verify kernel)."""
+        if not seqs:
+            return
+        starts = [0] * len(seqs) if starts is None else list(starts)
+        self.model.prefill([s.token_ids for s in seqs], starts, [getattr(s, self.table_attr) for s in seqs])
+
+    # ----------------------------------------------------------- draft loop
+    def _ensure_bufs(self, B: int, k: int, width: int) -> dict:
+        b = self._bufs
+        if b is not None and b["max_batch"] >= B and b["k"] == k and b["width"] >= width:
+            return b
+        mb = 1
+        while mb < B:
+            mb *= 2
+        if b is not None:
+            mb = max(mb, b["max_batch"])
+            width = max(width, b["width"])
+        dev, V = self.device, self.model.cfg.vocab_size
+        i64 = dict(dtype=torch.int64, device=dev)
+        b = {"max_batch": mb, "k": k, "width": width,
+             "ids0": torch.zeros(2 * mb, **i64), "pos0": torch.full((2 * mb,), -1, **i64),
+             "slot0": torch.full((2 * mb,), -1, **i64), "ctx0": torch.zeros(mb, **i64),
+             "pos": torch.full((k, mb), -1, **i64), "slot": torch.full((k, mb), -1, **i64),
+             "ctx": torch.zeros(k, mb, **i64),
+             "table": torch.full((mb, width), -1, dtype=torch.int32, device=dev),
+             "temps": torch.zeros(mb, dtype=torch.float32, device=dev),
+             "noise": torch.ones(mb, V, dtype=torch.float32, device=dev),
+             "tokens": torch.zeros(mb, k, dtype=torch.int32, device=dev),
+             "logits": torch.empty(k, mb, V, dtype=self.model.dtype, device=dev),
+             "cu2": torch.arange(0, 2 * mb + 1, 2, dtype=torch.int32, device=dev),
+             "cu1": torch.arange(0, mb + 1, dtype=torch.int32, device=dev)}
+        self._bufs = b
+        self._graphs = {}  # captured over the previous buffers
+        return b
+
+    def _body(self, b: dict, Bb: int, stochastic: bool, generator=None) -> None:
+        """The K steps over the first Bb rows of the static buffers: step 0
+        feeds positions (n-2, n-1) of every sequence, step i > 0 the token
+        step i - 1 sampled."""
+        from naivllm_amd.spec_engine.rejection_sampler import sample
+
+        k, m = b["k"], self.model
+        noise = b["noise"][:Bb]
+        tmp = m.forward(b["ids0"][:2 * Bb], b["pos0"][:2 * Bb], b["slot0"][:2 * Bb], b["table"][:Bb], b["ctx0"][:Bb],
+                        b["cu2"][:Bb + 1], 2)
+        b["logits"][0, :Bb].copy_(tmp[1::2])
+        for i in range(k):
+            if i > 0:
+                m.forward(b["tokens"][:Bb, i - 1], b["pos"][i, :Bb], b["slot"][i, :Bb], b["table"][:Bb],
+                          b["ctx"][i, :Bb], b["cu1"][:Bb + 1], 1, logits_out=b["logits"][i, :Bb])
+            if stochastic:
+                noise.exponential_(1, generator=generator).clamp_min_(1e-10)
+            sample(b["logits"][i, :Bb], b["temps"][:Bb], noise, out=b["tokens"][:Bb, i])
 
     @torch.inference_mode()
     def run_draft_steps(self, seqs, k: int, temperatures: torch.Tensor,
@@ -145,42 +201,77 @@ class DraftRunner:
         """K decode steps for ``seqs`` (n_b confirmed tokens each): step i
         feeds the token at position n_b-1+i and samples draft i+1; step 0
         also re-feeds position n_b-2 (see nsv_prepare_draft).  Returns the
-        per-sequence drafts and the logits buffer [k, B, V]."""
-        from naivllm_amd.spec_engine.rejection_sampler import sample
+        per-sequence drafts and the logits buffer [k, B, V] (valid until the
+        next call)."""
+        import numpy as np
 
-        dev, B = self.device, len(seqs)
-        table = self._table(seqs)
-        V = self.model.cfg.vocab_size
-        logit_buf = torch.empty(k, B, V, dtype=self.model.dtype, device=dev)
-        tokens = torch.empty(B, k, dtype=torch.int32, device=dev)
-        temps = temperatures.to(device=dev, dtype=torch.float32)
+        B = len(seqs)
+        temps = temperatures.to(dtype=torch.float32).cpu()
         stochastic = bool((temps > 1e-6).any())
-        noise = torch.ones(B, V, dtype=torch.float32, device=dev)
-        n = [len(s.token_ids) for s in seqs]
-        # step 0: rows (n-2, n-1) of every sequence
-        pos0 = [p for m in n for p in (m - 2, m - 1)]
-        ids0 = [s.token_ids[p] if p >= 0 else 0 for s, m in zip(seqs, n) for p in (m - 2, m - 1)]
-        pos0 = [p if p >= 0 else -1 for p in pos0]
-        slot0 = self._slots([s for s in seqs for _ in (0, 1)], pos0)
-        tmp = self.model.forward(torch.tensor(ids0, dtype=torch.int64, device=dev),
-                                 torch.tensor(pos0, dtype=torch.int64, device=dev),
-                                 torch.tensor(slot0, dtype=torch.int64, device=dev), table,
-                                 torch.tensor(n, dtype=torch.int64, device=dev),
-                                 torch.arange(0, 2 * B + 1, 2, dtype=torch.int32, device=dev), 2)
-        logit_buf[0].copy_(tmp[1::2])
-        cu1 = torch.arange(0, B + 1, dtype=torch.int32, device=dev)
-        for i in range(k):
-            if i > 0:
-                pos = [m - 1 + i for m in n]
-                self.model.forward(tokens[:, i - 1], torch.tensor(pos, dtype=torch.int64, device=dev),
-                                   torch.tensor(self._slots(seqs, pos), dtype=torch.int64, device=dev), table,
-                                   torch.tensor([p + 1 for p in pos], dtype=torch.int64, device=dev), cu1, 1,
-                                   logits_out=logit_buf[i])
-            if stochastic:
-                noise.exponential_(1, generator=generator).clamp_min_(1e-10)
-            sample(logit_buf[i], temps, noise, out=tokens[:, i])
-        host = tokens.cpu().tolist()  # the one synchronisation of the call
-        return host, logit_buf
+        tables = [getattr(s, self.table_attr) for s in seqs]
+        width = max(1, max(len(t) for t in tables))
+        b = self._ensure_bufs(B, k, width)
+        Bb = 1
+        while Bb < B:
+            Bb *= 2
+        # host staging of the call's metadata (pad rows inert)
+        n = np.array([len(s.token_ids) for s in seqs], dtype=np.int64)
+        p0 = np.stack([n - 2, n - 1], axis=1).reshape(-1)
+        ids0 = np.zeros(2 * Bb, dtype=np.int64)
+        pos0 = np.full(2 * Bb, -1, dtype=np.int64)
+        slot0 = np.full(2 * Bb, -1, dtype=np.int64)
+        for j, s in enumerate(seqs):
+            for r in (0, 1):
+                p = int(p0[2 * j + r])
+                if p >= 0:
+                    ids0[2 * j + r] = s.token_ids[p]
+                    pos0[2 * j + r] = p
+        slot0[:2 * B] = self._slots([s for s in seqs for _ in (0, 1)], pos0[:2 * B].tolist())
+        pos = np.full((k, Bb), -1, dtype=np.int64)
+        slot = np.full((k, Bb), -1, dtype=np.int64)
+        ctx = np.zeros((k, Bb), dtype=np.int64)
+        for i in range(1, k):
+            pi = (n - 1 + i).tolist()
+            pos[i, :B] = pi
+            slot[i, :B] = self._slots(seqs, pi)
+            ctx[i, :B] = n + i
+        ctx0 = np.zeros(Bb, dtype=np.int64)
+        ctx0[:B] = n
+        table = np.full((Bb, b["width"]), -1, dtype=np.int32)
+        for j, row in enumerate(tables):
+            table[j, :len(row)] = row
+        tv = np.zeros(Bb, dtype=np.float32)
+        tv[:B] = temps.numpy()
+        dev = self.device
+        t = lambda x: torch.from_numpy(x).to(dev, non_blocking=False)  # noqa: E731
+        b["ids0"][:2 * Bb].copy_(t(ids0))
+        b["pos0"][:2 * Bb].copy_(t(pos0))
+        b["slot0"][:2 * Bb].copy_(t(slot0))
+        b["ctx0"][:Bb].copy_(t(ctx0))
+        b["pos"][:, :Bb].copy_(t(pos))
+        b["slot"][:, :Bb].copy_(t(slot))
+        b["ctx"][:, :Bb].copy_(t(ctx))
+        b["table"][:Bb].copy_(t(table))
+        b["temps"][:Bb].copy_(t(tv))
+        if not stochastic:
+            b["noise"][:Bb].fill_(1.0)
+        if not self.use_graphs or (stochastic and generator is not None):
+            self._body(b, Bb, stochastic, generator)
+        else:
+            key = (Bb, stochastic)
+            graph = self._graphs.get(key)
+            if graph is None:
+                self._body(b, Bb, stochastic)  # warm-up (workspaces sized); its results stand for this call
+                torch.cuda.synchronize(dev)
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
+                    self._body(b, Bb, stochastic)
+                self._graphs[key] = graph
+                # the capture did not run; this call's results are the warm-up's
+            else:
+                graph.replay()
+        host = b["tokens"][:B].cpu().tolist()  # the one synchronisation of the call
+        return host, b["logits"][:, :B]
 
 
 class ModelDrafter:

@@ -93,13 +93,68 @@ def test_decode_step_through_set_context():
     assert_close(out.view(-1, vb.num_heads, vb.head_dim), want, "bf16", "decode via set_context")
 
 
-def test_prefill_context_is_refused():
-    layer = Attention(16, 128, num_kv_heads=8, block_size=256)
-    set_context(True, cu_seqlens_q=torch.tensor([0, 4], dtype=torch.int32, device="cuda"))
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_prefill_step_through_set_context_paged(dtype):
+    # the reference's paged prefill (layers/attention.py:741-752): two prompts,
+    # the second behind a 2-page cached prefix; the step stores its K/V at the
+    # slots, then every new row attends its sequence's keys 0 .. its position
+    print(f"case: Attention paged prefill via set_context {dtype}", flush=True)
+    lens, cached = [300, 1210], [0, 128]
+    vb = synth.verify_batch(33, lens, [n - c for n, c in zip(lens, cached)], block_size=64, dtype=dtype)
+    layer, f = _layer(vb)
+    if dtype == "f32":
+        f = lambda x: torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).cuda()  # noqa: E731
+        layer.k_cache, layer.v_cache = f(vb.k_cache), f(vb.v_cache)
+    slots = _slots(vb, vb.positions)
+    k, v = _new_kv(vb, 33)
+    qlens = [n - c for n, c in zip(lens, cached)]
+    set_context(True, cu_seqlens_q=torch.from_numpy(vb.cu_seqlens_q).cuda(),
+                cu_seqlens_k=torch.tensor([0, lens[0], sum(lens)], dtype=torch.int32, device="cuda"),
+                max_seqlen_q=max(qlens), max_seqlen_k=max(lens), slot_mapping=torch.from_numpy(slots).cuda(),
+                block_tables=torch.from_numpy(vb.block_tables).cuda(), seqlens_q=qlens, seqlens_k=lens)
     try:
-        with pytest.raises(ValueError, match="prefill"):
-            layer(torch.zeros(4, 16 * 128, device="cuda", dtype=torch.bfloat16),
-                  torch.zeros(4, 8 * 128, device="cuda", dtype=torch.bfloat16),
-                  torch.zeros(4, 8 * 128, device="cuda", dtype=torch.bfloat16))
+        out = layer(f(vb.q), f(k), f(v))
+        torch.cuda.synchronize()
     finally:
         reset_context()
+    kc, vc = vb.k_cache.copy(), vb.v_cache.copy()
+    ora.store_kvcache(k, v, kc, vc, slots)
+    want = ora.verify_attention(vb.q, kc, vc, vb.block_tables, vb.context_lens, vb.cu_seqlens_q, vb.positions,
+                                1 / np.sqrt(vb.head_dim), vb.num_heads, vb.num_kv_heads)
+    assert_close(out.view(-1, vb.num_heads, vb.head_dim), want, dtype, "paged prefill via set_context")
+    assert torch.equal(layer.k_cache.float().cpu(), torch.from_numpy(kc).float())
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_prefill_step_through_set_context_contiguous(dtype):
+    # no block tables (no cached prefix): the reference's varlen flash path
+    # (layers/attention.py:754) over the step's own contiguous K/V; a
+    # 1100-key prompt needs more than one key split and more than one
+    # causal block
+    print(f"case: Attention varlen prefill via set_context {dtype}", flush=True)
+    H, Hkv, D = 16, 8, 128
+    lens = [37, 1100, 5]
+    T = sum(lens)
+    rnd = lambda st, n: synth.round_to(synth.normal(34, st, n), dtype)  # noqa: E731
+    q = rnd(1, T * H * D).reshape(T, H, D)
+    k = rnd(2, T * Hkv * D).reshape(T, Hkv, D)
+    v = rnd(3, T * Hkv * D).reshape(T, Hkv, D)
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    f = lambda x: torch.from_numpy(np.ascontiguousarray(x, dtype=np.float32)).cuda().to(tdt)  # noqa: E731
+    layer = Attention(H, D, scale=1.0, num_kv_heads=Hkv, block_size=256)  # no cache allocated
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    set_context(True, cu_seqlens_q=torch.from_numpy(cu).cuda(), cu_seqlens_k=torch.from_numpy(cu).cuda(),
+                max_seqlen_q=max(lens), max_seqlen_k=max(lens), seqlens_q=lens, seqlens_k=lens)
+    try:
+        out = layer(f(q), f(k), f(v))
+        torch.cuda.synchronize()
+    finally:
+        reset_context()
+    # oracle: each sequence as its own one-page cache
+    want = []
+    for i, n in enumerate(lens):
+        sl = slice(cu[i], cu[i + 1])
+        want.append(ora.verify_attention(q[sl], k[sl][None], v[sl][None], np.zeros((1, 1), np.int32),
+                                         np.array([n]), np.array([0, n], np.int32), np.arange(n),
+                                         1 / np.sqrt(D), H, Hkv))
+    assert_close(out.view(-1, H, D), np.concatenate(want), dtype, "varlen prefill via set_context")

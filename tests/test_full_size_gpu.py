@@ -101,7 +101,7 @@ def _load_round(eng, r, prompts, sp):
     return hists
 
 
-@pytest.mark.parametrize("batch", [1, 8])
+@pytest.mark.parametrize("batch", [1, 2, 4, 8])
 def test_config3_round_matches_host_restatement(batch):
     print(f"case: config3 eager round b{batch} vs host restatement (Qwen3-0.6B)", flush=True)
     K = 8
@@ -124,7 +124,7 @@ def test_config3_round_matches_host_restatement(batch):
     print(f"  drafted {[len(d) for d in drafts]} accepted {[len(a) for a in accepted]}", flush=True)
 
 
-@pytest.mark.parametrize("batch", [1, 8])
+@pytest.mark.parametrize("batch", [1, 2, 4, 8])
 def test_config3_spec_equals_plain_and_graph_equals_eager(batch):
     print(f"case: config3 b{batch}: 48 greedy tokens, spec == plain, graph == eager (Qwen3-0.6B)", flush=True)
     base = dict(num_speculative_tokens=8, ngram_min_size=2, ngram_max_size=4, max_num_sequences=batch,

@@ -245,3 +245,41 @@ def test_drop_in_model_and_hybrid_drafters():
     assert lists[0] == ng[0] and rows[0] is None
     assert len(lists[1]) == K and rows[1] is not None and rows[1].shape == (K, DRAFT.vocab_size)
     assert hyb.model_rounds == 1 and hyb.model_seqs == 1
+
+
+def test_draft_runner_graphs_match_eager():
+    # the graphed K-step draft loop (one graph per batch bucket, replayed from
+    # static buffers) against the eager loop on identical weights: identical
+    # greedy drafts and logits, for 3 sequences (bucket 4, one inert pad row)
+    # over three calls (capture, then two replays with new lengths), then 1
+    print("case: DraftRunner graphs == eager", flush=True)
+    from naivllm_amd.engine.block_manager import BlockManager
+    from naivllm_amd.layers.qwen3 import Qwen3Verify
+    from naivllm_amd.spec_engine import DraftRunner
+
+    K = 5
+    runs = {}
+    for graphed in (True, False):
+        dm = Qwen3Verify(DRAFT, "cuda", seed=23)
+        runner = DraftRunner(dm, num_blocks=64, block_size=16, use_graphs=graphed)
+        bm = BlockManager(64, 16, table_attr="draft_block_table", cached_attr="draft_num_cached_tokens")
+        seqs = [Sequence(list(p[:20 + 7 * i])) for i, p in enumerate(prompts_with_spans(14, 3))]
+        for s in seqs:
+            bm.allocate(s)
+            bm.ensure_capacity(s, len(s) + 3 * (K + 1))
+        runner.prefill(seqs)
+        out = []
+        temps = torch.zeros(len(seqs))
+        for call in range(3):
+            toks, logits = runner.run_draft_steps(seqs, K, temps)
+            out.append((toks, logits.float().cpu().clone()))
+            for s, t in zip(seqs, toks):  # commit two drafts, as an acceptance would
+                s.append_token(t[0])
+                s.append_token(t[1])
+        toks, logits = runner.run_draft_steps(seqs[:1], K, temps[:1])
+        out.append((toks, logits.float().cpu().clone()))
+        runs[graphed] = out
+        assert (len(runner._graphs) == 2) == graphed  # buckets 4 and 1
+    for (tg, lg), (te, le) in zip(runs[True], runs[False]):
+        assert tg == te
+        assert torch.equal(lg, le)

@@ -11,6 +11,7 @@ from naivllm_amd.engine.model_runner import ModelRunner
 from naivllm_amd.engine.sequence import Sequence
 from naivllm_amd.layers.qwen3 import Qwen3Config, Qwen3Verify
 from naivllm_amd.utils import synth
+from naivllm_amd.utils.context import get_context, reset_context
 
 pytestmark = pytest.mark.gpu
 
@@ -63,8 +64,21 @@ def test_graphed_rows_at_stride_k_plus_1():
     # eager: packed rows, equal to a direct forward on the packed rows
     eager = ModelRunner(model, max_num_sequences=4, num_spec_tokens=K, max_model_length=256, enforce_eager=True)
     packed = eager.run_spec_verify(seqs)
-    ids, pos, slots, bt, ctx, cu, mq = eager.prepare_spec_verify(seqs)
-    assert torch.equal(packed, model.forward(ids, pos, slots, bt, ctx, cu, mq))
+    assert not get_context().is_verify  # run_spec_verify resets the context after its forward
+    # prepare_spec_verify publishes the step's Context (model_runner.py:467-480) and returns the input_ids
+    ids = eager.prepare_spec_verify(seqs)
+    c = get_context()
+    try:
+        assert c.is_prefill and c.is_verify and c.cu_seqlens_k is None
+        assert c.seqlens_q == [len(s.draft_tokens) + 1 for s in seqs] and c.seqlens_k == [len(s) for s in seqs]
+        assert c.max_seqlen_q == max(c.seqlens_q) and c.max_seqlen_k == max(c.seqlens_k)
+        assert ids.dtype == torch.int64 and ids.shape[0] == sum(c.seqlens_q)
+        assert c.positions.tolist() == [p for s in seqs for p in range(len(s) - len(s.draft_tokens) - 1, len(s))]
+        want_packed = model.forward(ids, c.positions, c.slot_mapping, c.block_tables, c.context_lens,
+                                    c.cu_seqlens_q, c.max_seqlen_q)
+    finally:
+        reset_context()
+    assert torch.equal(packed, want_packed)
     assert packed.shape[0] == sum(len(s.draft_tokens) + 1 for s in seqs)
     # the two layouts agree row for row (bf16 logits of two batch shapes)
     r = 0
