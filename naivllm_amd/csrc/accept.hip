@@ -120,7 +120,7 @@ __device__ __forceinline__ void load_slab(const T* row, int64_t lo, int64_t hi, 
       const int64_t v0 = slab_index(lo, g * kGroup);
 #pragma unroll
       for (int l = 0; l < L; ++l)
-        w[g][l] = v0 + kGroup <= hi ? *reinterpret_cast<const u32x4*>(row + v0 + l * PER) : u32x4{0u, 0u, 0u, 0u};
+        w[g][l] = v0 + kGroup <= hi ? load16_stream(row + v0 + l * PER) : u32x4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
     for (int g = 0; g < G; ++g) {

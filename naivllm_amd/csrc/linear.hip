@@ -173,7 +173,7 @@ __global__ __launch_bounds__(kLinThreads, lin_waves_per_eu(MT, SMALL, BNV)) void
     ch.in = k0 + KC <= K || k0 + cc * 8 < K;
     const int kk = ch.in ? k0 : -cc * 8;
 #pragma unroll
-    for (int j = 0; j < WL; ++j) ch.wv[j] = *reinterpret_cast<const u32x4*>(wp[j] + kk);
+    for (int j = 0; j < WL; ++j) ch.wv[j] = load16_stream(wp[j] + kk);
 #pragma unroll
     for (int j = 0; j < AL; ++j) ch.xv[j] = *reinterpret_cast<const u32x4*>(xp[j] + kk);
     if constexpr (NORM) ch.nv = *reinterpret_cast<const u32x4*>(a.norm_w + kk + cc * 8);
@@ -668,7 +668,7 @@ __global__ __launch_bounds__(kStreamWaves * 64, 1) void stream_linear_kernel(Str
   auto wrow = [&](int i) { return a.w + ((int64_t)(gw + min(i, my_tiles - 1) * nwaves) * 16 + c) * K + 8 * g4; };
   auto issue = [&](u32x4 (&buf)[8], const uint16_t* p) {
 #pragma unroll
-    for (int s = 0; s < 8; ++s) buf[s] = *reinterpret_cast<const u32x4*>(p + 32 * s);
+    for (int s = 0; s < 8; ++s) buf[s] = load16_stream(p + 32 * s);
   };
   f32x4 acc[MT];
 #pragma unroll
@@ -798,11 +798,11 @@ __global__ __launch_bounds__(kDecodeWaves * 64) void decode_linear_kernel(Linear
   u32x4 wv[KL], uv[EPI == 1 ? KL : 1], xv[MR][KL], nv[NORM ? KL : 1];
   const uint16_t* wr = a.w + (int64_t)col * K + lane * 8;
 #pragma unroll
-  for (int i = 0; i < KL; ++i) wv[i] = *reinterpret_cast<const u32x4*>(wr + i * 512);
+  for (int i = 0; i < KL; ++i) wv[i] = load16_stream(wr + i * 512);
   if constexpr (EPI == 1) {
     const uint16_t* ur = a.w + (int64_t)(a.N / 2 + col) * K + lane * 8;
 #pragma unroll
-    for (int i = 0; i < KL; ++i) uv[i] = *reinterpret_cast<const u32x4*>(ur + i * 512);
+    for (int i = 0; i < KL; ++i) uv[i] = load16_stream(ur + i * 512);
   }
 #pragma unroll
   for (int m = 0; m < MR; ++m)

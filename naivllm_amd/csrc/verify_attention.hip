@@ -130,6 +130,7 @@ struct VerifyArgs {
 
 __device__ __forceinline__ u32x4 load16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
 
+
 // A float pair as one 64-bit agent-scope (device-coherent) relaxed atomic
 // store: coherent across XCDs without cache maintenance instructions.
 __device__ __forceinline__ void store_agent(uint64_t* p, float x, float y) {
@@ -441,7 +442,7 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
         const int id = j * NSV_WAVE + lane;
         const int r = id / VCH, ch = id - r * VCH;
         const unsigned off = (base_key + (r < nvalid ? r : 0)) * row_bytes + ch * 16;
-        T.v[j] = load16(vp + off);
+        T.v[j] = load16_stream(vp + off);  // (K stays cached: the pair's other slices read it)
       }
     } else {
       const int n = T.n0 + lane;
@@ -468,7 +469,7 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
         const int pv = __shfl(pg, r, NSV_WAVE);
         const int64_t row = ((T.kmask >> r) & 1) ? (int64_t)pv * page_elems + (int64_t)((T.n0 + r) & bs_mask) * tok_stride
                                                  : dflt;
-        T.v[j] = load16(vbase + row + ch * 8);
+        T.v[j] = load16_stream(vbase + row + ch * 8);
       }
     }
   };
@@ -1012,18 +1013,18 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
 #pragma unroll
       for (int j = 0; j < KS; ++j) {  // 16 keys x VCH chunks = KS loads of 64 chunks
         const int r = j * KPI + lane / VCH, ch = lane % VCH;
-        T.k[j] = load16(kp + (base_key + (r < nvalid ? r : 0)) * row_bytes + ch * 16);
+        T.k[j] = load16_stream(kp + (base_key + (r < nvalid ? r : 0)) * row_bytes + ch * 16);
       }
     } else {
       const unsigned off = (base_key + (c < nvalid ? c : 0)) * row_bytes + g4 * 16;
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) T.k[ks] = load16(kp + off + ks * 64);
+      for (int ks = 0; ks < KS; ++ks) T.k[ks] = load16_stream(kp + off + ks * 64);
     }
 #pragma unroll
     for (int j = 0; j < VL; ++j) {
       const int r = j * KPI + lane / VCH, ch = lane % VCH;
       const unsigned off = (base_key + (r < nvalid ? r : 0)) * row_bytes + ch * 16;
-      T.v[j] = load16(vp + off);
+      T.v[j] = load16_stream(vp + off);
     }
   };
 
@@ -1924,8 +1925,8 @@ __global__ __launch_bounds__(512) void attn_load_floor_kernel(VerifyArgs a, uint
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int key = ((n0 & bs_mask) + j * 4 + (lane >> 4));
-      kv[j] = load16((const char*)a.k_cache + base + (size_t)key * row_bytes);
-      kv[4 + j] = load16((const char*)a.v_cache + base + (size_t)key * row_bytes);
+      kv[j] = load16_stream((const char*)a.k_cache + base + (size_t)key * row_bytes);
+      kv[4 + j] = load16_stream((const char*)a.v_cache + base + (size_t)key * row_bytes);
     }
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc ^= kv[j];
@@ -1945,11 +1946,11 @@ __global__ __launch_bounds__(512) void stream_read_kernel(const char* buf, size_
   for (; off + 3 * step + 16 <= end; off += 4 * step) {
     u32x4 t[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) t[u] = load16(buf + off + u * step);
+    for (int u = 0; u < 4; ++u) t[u] = load16_stream(buf + off + u * step);
 #pragma unroll
     for (int u = 0; u < 4; ++u) acc ^= t[u];
   }
-  for (; off + 16 <= end; off += step) acc ^= load16(buf + off);
+  for (; off + 16 <= end; off += step) acc ^= load16_stream(buf + off);
   const uint32_t x = acc.x ^ acc.y ^ acc.z ^ acc.w;
   if (x == 0x9e3779b9u) sink[blockIdx.x] = x;
 }
