@@ -559,6 +559,7 @@ def rejection_sampling(seed: int = 2, sets: int = 8) -> dict:
         for x in ins:
             accept_greedy(x["target"], x["drafts"], nd, K + 1, out_tokens=out_t, out_len=out_n)
 
+    margins = _decision_margins(ins, nd, temp, out_t, out_n)
     st_us = _graph_us(stoch_step, sets, steps=20)
     gr_us = _graph_us(greedy_step, sets, steps=20)
     st_bytes = B * (K + 1) * V * 2 + B * K * V * 2 + B * V * 2 + B * K * 4 * 2 + B * 4 + B * (K + 2) * 4 + B * 4
@@ -571,8 +572,70 @@ def rejection_sampling(seed: int = 2, sets: int = 8) -> dict:
             "greedy": {"us_per_call": round(gr_us, 3), "bytes_per_call": gr_bytes,
                        "GBs": round(gr_bytes / gr_us / 1e3, 1),
                        "frac": round(gr_bytes / gr_us / 1e3 / HBM_PEAK_GBS, 4)},
+            "decision_margins": margins,
             "workload": "config 2 acceptance: B=8, K=8 model drafts, V=151936, bf16 logits, T=1, "
                         f"{sets} rotating input sets"}
+
+
+def _bf16_round_margin(p: torch.Tensor) -> torch.Tensor:
+    """Relative distance of fp64 values p > 0 to the nearest bf16 rounding
+    boundary (a midpoint between neighbouring bf16 values): how far an error
+    in p may go before its bf16 rounding changes."""
+    e = torch.floor(torch.log2(p))
+    ulp = torch.exp2(e - 7)
+    r = p / ulp  # in [128, 256)
+    return (torch.abs(r - torch.floor(r) - 0.5) * ulp) / p
+
+
+def _decision_margins(ins, nd, temp, out_t, out_n) -> dict:
+    """How close config 2's acceptance decisions came to flipping, from the
+    same inputs the kernel consumed (torch on the GPU, fp64): for every
+    decided draft (the accepted prefix and the first rejection) the margin
+    |u - min(1, p_t/p_d)| against the ratio's bf16 ulp, and the relative
+    distance of p_t and p_d (exact softmax values) to a bf16 rounding
+    boundary; for every sampled row the relative gap between the two
+    largest p / q (the multinomial's argmax).  A decision whose margin is
+    inside these bands is one that a different softmax reduction order (the
+    reference's fp32 torch softmax against this library's exact-then-rounded
+    contract) could decide otherwise."""
+    from naivllm_amd.spec_engine.rejection_sampler import accept_stochastic
+
+    B, K = nd.shape[0], int(nd[0])
+    n_dec, n_band = 0, 0
+    min_abs, min_round, min_gap = float("inf"), float("inf"), float("inf")
+    for x in ins:
+        accept_stochastic(x["target"], x["drafts"], nd, temp, x["noise"], uniforms=x["uniforms"],
+                          draft_logits=x["draft"], target_seq_stride=K + 1, draft_seq_stride=K, draft_row_stride=1,
+                          out_tokens=out_t, out_len=out_n)
+        V = x["target"].shape[-1]
+        pt = torch.softmax(x["target"].view(B, K + 1, V).double(), -1)
+        pd = torch.softmax(x["draft"].view(B, K, V).double(), -1)
+        lens = out_n.tolist()
+        for b in range(B):
+            acc = lens[b] - 1  # drafts accepted
+            for i in range(min(acc + 1, K)):
+                d = int(x["drafts"][b, i])
+                a, c = pt[b, i, d], pd[b, i, d]
+                ab, cb = a.to(torch.bfloat16).float(), c.to(torch.bfloat16).float()
+                ratio = torch.clamp((ab / torch.clamp(cb, min=1e-20)).to(torch.bfloat16).float(), max=1.0)
+                u = float(x["uniforms"][b, i])
+                m = abs(u - float(ratio))
+                ulp = 2.0 ** (float(torch.floor(torch.log2(ratio))) - 7)
+                n_dec += 1
+                n_band += int(m < ulp)
+                min_abs = min(min_abs, m)
+                min_round = min(min_round, float(_bf16_round_margin(torch.stack([a, c])).min()))
+            r = min(acc, K)  # the resampled (rejection) or bonus row
+            if acc < K:
+                prob = torch.clamp(pt[b, r] - pd[b, r], min=0)
+                prob = prob / prob.sum()
+            else:
+                prob = pt[b, r]
+            top = torch.topk(prob / x["noise"][b].double(), 2).values
+            min_gap = min(min_gap, float((top[0] - top[1]) / top[0]))
+    return {"decisions": n_dec, "min_abs_margin": min_abs, "within_one_bf16_ulp_of_ratio": n_band,
+            "min_rel_distance_to_bf16_rounding": min_round, "samples": len(ins) * B,
+            "min_rel_top2_gap_of_sample": min_gap}
 
 
 def copy_probe(mib: int) -> None:
