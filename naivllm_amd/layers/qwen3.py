@@ -12,9 +12,11 @@ pre-attention epilogue (q/k RMSNorm + RoPE + paged KV store), verify
 attention, o_proj (with the residual add as its epilogue), gate_up
 (post-attention RMSNorm prologue, SiLU * up epilogue) and down (residual
 add epilogue).  Wider batches run the projections on hipBLASLt between
-this library's residual-RMSNorm, epilogue, attention and SiLU kernels; the
-LM head is hipBLASLt in both.  Weights are random (seeded): no checkpoint
-is loaded.
+this library's residual-RMSNorm, epilogue, attention and SiLU kernels.  The
+LM head runs on this library's streaming kernel up to lm_head_rows() rows
+(79 at hidden 1024, 19 at hidden 4096: the activations staged in one CU's
+LDS), on hipBLASLt beyond.  Weights are random (seeded): no checkpoint is
+loaded.
 
 The forward takes the verify metadata explicitly (positions, slots, block
 tables, context lengths, cu_seqlens) so a whole forward is capturable in a
