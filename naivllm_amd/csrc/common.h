@@ -29,6 +29,15 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
   return __uint_as_float(bits16 << 16);
 }
 
+// Two floats to packed bf16 (lo in the low half), round to nearest even: one
+// v_cvt_pk_bf16_f32 on gfx950.  The same values as f32_to_bf16_bits below
+// for every non-NaN input (a NaN comes out as a quiet NaN either way).
+typedef float f32x2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2v){lo, hi}, bf16x2v));
+}
+
 // Round-to-nearest-even narrowing (NaN kept quiet), the rounding torch and
 // the reference's Triton `.to(bfloat16)` apply.
 __device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {

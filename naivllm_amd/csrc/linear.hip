@@ -63,13 +63,7 @@ struct LinearArgs {
 };
 
 __device__ __forceinline__ bf16x8 to_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
-typedef float f32x2v __attribute__((ext_vector_type(2)));
-typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
-// two floats to packed bf16, round to nearest even (gfx950's v_cvt_pk_bf16_f32)
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2v){lo, hi}, bf16x2v));
-}
 __device__ __forceinline__ float bfv(uint32_t word, int hi) { return __uint_as_float(hi ? (word & 0xffff0000u) : (word << 16)); }
 
 // Chunk size and occupancy.  A grid of more workgroups than CUs (384 for

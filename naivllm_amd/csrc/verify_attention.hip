@@ -283,21 +283,35 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
   constexpr int MERGE = MTP * MTILE_BYTES;
   constexpr int SMEM = STAGE > MERGE ? STAGE : MERGE;
 
-  __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM];
-  __shared__ int pages[kMaxSplitPages];
-  __shared__ float red_m[NW][MP];
-  __shared__ float red_l[NW][MP];
-  __shared__ float row_l[MP];
-  __shared__ float row_ms[MP];
-  __shared__ int row_pos[MP];
-  __shared__ int ds_last;
   // PARK: each wave parks its unscaled O slice and (max, sum) in LDS of its
   // own as soon as its tiles are done, while slower waves still stream; one
   // barrier later every output is the factor-weighted sum of the parked
   // slices.  Taken when the parking area fits beside the staging area.
   constexpr int PARK_FLOATS = NW * MP * RSTR;
   constexpr bool PARK = SMEM + PARK_FLOATS * 4 + kMaxSplitPages * 4 + 2 * NW * MP * 4 + 3 * MP * 4 <= 159 * 1024;
-  __shared__ __attribute__((aligned(16))) float park[PARK ? PARK_FLOATS : 4];
+  // One LDS block, the small arrays first: their addresses then fit the
+  // 16-bit offset field of the LDS instructions.
+  struct __attribute__((aligned(16))) Lds {
+    float red_m[NW][MP];
+    float red_l[NW][MP];
+    float row_l[MP];
+    float row_ms[MP];
+    int row_pos[MP];
+    int ds_last;
+    int pages[kMaxSplitPages];
+    __attribute__((aligned(16))) unsigned char smem[SMEM];
+    __attribute__((aligned(16))) float park[PARK ? PARK_FLOATS : 4];
+  };
+  __shared__ Lds lds;
+  auto& red_m = lds.red_m;
+  auto& red_l = lds.red_l;
+  auto& row_l = lds.row_l;
+  auto& row_ms = lds.row_ms;
+  auto& row_pos = lds.row_pos;
+  auto& ds_last = lds.ds_last;
+  auto& pages = lds.pages;
+  unsigned char* const smem = lds.smem;
+  float* const park = lds.park;
 
   // ---- workgroup -> (pair, dq, split); every workgroup of a pair on one XCD
   const int wg = blockIdx.x;
@@ -694,8 +708,8 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
     for (int j = 0; j < ITEMS; ++j) {
       if (!iok[j]) continue;
       const float inv = den[j] > 0.f ? 1.f / den[j] : 0.f;
-      const uint32_t lo = (uint32_t)f32_to_bf16_bits(num[j][0] * inv) | ((uint32_t)f32_to_bf16_bits(num[j][1] * inv) << 16);
-      const uint32_t hi = (uint32_t)f32_to_bf16_bits(num[j][2] * inv) | ((uint32_t)f32_to_bf16_bits(num[j][3] * inv) << 16);
+      const uint32_t lo = pack_bf16x2(num[j][0] * inv, num[j][1] * inv);
+      const uint32_t hi = pack_bf16x2(num[j][2] * inv, num[j][3] * inv);
       *idst[j] = make_uint2(lo, hi);
     }
   };
@@ -727,8 +741,8 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
         if (t >= qlen) continue;
         const float inv = (L > 0.f && row_pos[m] >= 0) ? 1.f / L : 0.f;
         bf16_t* dst = (bf16_t*)a.out + ((int64_t)(q0 + t) * a.H + hk * a.Gs + a.g0 + g) * DH + dq * DC + c4 * 4;
-        const uint32_t lo = (uint32_t)f32_to_bf16_bits(o[0] * inv) | ((uint32_t)f32_to_bf16_bits(o[1] * inv) << 16);
-        const uint32_t hi = (uint32_t)f32_to_bf16_bits(o[2] * inv) | ((uint32_t)f32_to_bf16_bits(o[3] * inv) << 16);
+        const uint32_t lo = pack_bf16x2(o[0] * inv, o[1] * inv);
+        const uint32_t hi = pack_bf16x2(o[2] * inv, o[3] * inv);
         *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
       } else {
         if (row_pos[m] < 0) o = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -796,8 +810,8 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
         const float L = row_l[m];
         const float inv = (L > 0.f && row_pos[m] >= 0) ? 1.f / L : 0.f;
         bf16_t* dst = (bf16_t*)a.out + ((int64_t)(q0 + t) * a.H + hk * a.Gs + a.g0 + g) * DH + dq * DC + c4 * 4;
-        const uint32_t lo = (uint32_t)f32_to_bf16_bits(o[0] * inv) | ((uint32_t)f32_to_bf16_bits(o[1] * inv) << 16);
-        const uint32_t hi = (uint32_t)f32_to_bf16_bits(o[2] * inv) | ((uint32_t)f32_to_bf16_bits(o[3] * inv) << 16);
+        const uint32_t lo = pack_bf16x2(o[0] * inv, o[1] * inv);
+        const uint32_t hi = pack_bf16x2(o[2] * inv, o[3] * inv);
         *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
       } else {
         if (row_pos[m] < 0) o = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -858,18 +872,34 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
   constexpr int MERGE_BYTES = NW * MROWS * RSTR * 4;  // every wave's O for MROWS rows
   constexpr int SMEM = STAGE > MERGE_BYTES ? STAGE : MERGE_BYTES;
 
-  __shared__ __attribute__((aligned(16))) unsigned char smem[SMEM];
-  __shared__ int pages[kMaxSplitPages];
-  __shared__ float red_m[NW][MP];
-  __shared__ float red_l[NW][MP];
-  __shared__ float row_l[MP];
-  __shared__ float row_ms[MP];
-  __shared__ int row_pos[MP];
-  // The workgroup's query rows, the B operand of S^T, shared by the 8 waves
-  // (held in registers they would take 4 KS VGPRs per m-tile from the K/V
-  // pipeline); chunk X of row m at slot X ^ (m % VCH), so the 16 rows a
-  // B-operand read touches fall in distinct banks.
-  __shared__ __attribute__((aligned(16))) unsigned char q_lds[MP * DH * 2];
+  // One LDS block, the small arrays first: their addresses then fit the
+  // 16-bit offset field of the LDS instructions, so the merge addresses them
+  // from one base register instead of computing each address.
+  struct __attribute__((aligned(16))) Lds {
+    float red_m[NW][MP];
+    float red_l[NW][MP];
+    float row_l[MP];
+    float row_ms[MP];
+    int row_pos[MP];
+    int is_last;
+    int pages[kMaxSplitPages];
+    // The workgroup's query rows, the B operand of S^T, shared by the 8 waves
+    // (held in registers they would take 4 KS VGPRs per m-tile from the K/V
+    // pipeline); chunk X of row m at slot X ^ (m % VCH), so the 16 rows a
+    // B-operand read touches fall in distinct banks.
+    __attribute__((aligned(16))) unsigned char q_lds[MP * DH * 2];
+    __attribute__((aligned(16))) unsigned char smem[SMEM];
+  };
+  __shared__ Lds lds;
+  auto& red_m = lds.red_m;
+  auto& red_l = lds.red_l;
+  auto& row_l = lds.row_l;
+  auto& row_ms = lds.row_ms;
+  auto& row_pos = lds.row_pos;
+  auto& is_last = lds.is_last;
+  auto& pages = lds.pages;
+  unsigned char* const q_lds = lds.q_lds;
+  unsigned char* const smem = lds.smem;
 
   // ---- workgroup -> (pair, split); every split of a pair on one XCD
   const int wg = blockIdx.x;
@@ -1090,8 +1120,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
       l_run[mt] = fmaf(l_run[mt], alpha[mt], row_sum4((p[0] + p[1]) + (p[2] + p[3])));
       m_run[mt] = m_new;
       // P^T as the B operand, rounded to bf16 like the reference's p.to(v.dtype)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) pB[mt][i] = (short)f32_to_bf16_bits(p[i]);
+      pB[mt] = __builtin_bit_cast(i16x4, make_uint2(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])));
     }
     bool moved = false;
 #pragma unroll
@@ -1241,8 +1270,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
         const float L = row_l[m];
         const float inv = L > 0.f ? 1.f / L : 0.f;
         bf16_t* dst = (bf16_t*)a.out + ((int64_t)(q0 + t) * a.H + hk * a.Gs + a.g0 + g) * DH + c4 * 4;
-        const uint32_t lo = (uint32_t)f32_to_bf16_bits(o[0] * inv) | ((uint32_t)f32_to_bf16_bits(o[1] * inv) << 16);
-        const uint32_t hi = (uint32_t)f32_to_bf16_bits(o[2] * inv) | ((uint32_t)f32_to_bf16_bits(o[3] * inv) << 16);
+        const uint32_t lo = pack_bf16x2(o[0] * inv, o[1] * inv);
+        const uint32_t hi = pack_bf16x2(o[2] * inv, o[3] * inv);
         *reinterpret_cast<uint2*>(dst) = make_uint2(lo, hi);
       } else {
         store16_agent(prs, (unsigned)(m * DH + c4 * 4) * 4u, o);
@@ -1298,7 +1327,6 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
   // the counter's value came back, so it reads every other split's partials.
   __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  __shared__ int is_last;
   if (tid == 0)
     is_last = __hip_atomic_fetch_add(&a.counters[counter_slot(pair)], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
               (unsigned)(nsplit - 1);
@@ -1323,8 +1351,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
   };
   auto emit = [&](uint2* dst, float den, f32x4 num) {
     const float inv = den > 0.f ? 1.f / den : 0.f;
-    const uint32_t lo = (uint32_t)f32_to_bf16_bits(num[0] * inv) | ((uint32_t)f32_to_bf16_bits(num[1] * inv) << 16);
-    const uint32_t hi = (uint32_t)f32_to_bf16_bits(num[2] * inv) | ((uint32_t)f32_to_bf16_bits(num[3] * inv) << 16);
+    const uint32_t lo = pack_bf16x2(num[0] * inv, num[1] * inv);
+    const uint32_t hi = pack_bf16x2(num[2] * inv, num[3] * inv);
     *dst = make_uint2(lo, hi);
   };
   // a real split other than this one (its values are loaded and not used)
