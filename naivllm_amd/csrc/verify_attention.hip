@@ -69,6 +69,9 @@ constexpr int bf16_stages(int MT, int DH, int DC, bool UPAGE) {
   return want < 2 ? 2 : (want > fit ? (fit < 2 ? 2 : fit) : want);
 }
 constexpr float kNegInf = -__builtin_inff();
+// how far (log2 domain) a row's running maximum may pass its exponent reference
+// before the key-split kernel moves the reference (weights stay <= 2^8)
+constexpr float kRefSlack = 8.f;
 
 // Timeline stamps (a build knob: libnaivspec_stamp.so is built with
 // NSV_STAMP=1; the default library has no stamp code).  Thread 0 of every
@@ -992,7 +995,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
     qmin = __builtin_amdgcn_readfirstlane(qmin);
   };
 
-  float m_run[MT], l_run[MT];  // running max of raw scores, running sum
+  float m_run[MT], l_run[MT];  // exponent reference (raw-score units; -inf until a finite score), running sum
   f32x4 acc[DT][MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
@@ -1105,26 +1108,37 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
           sacc[mt][i] = (r < T.nvalid && T.n0 + r <= qpos[mt]) ? sacc[mt][i] : kNegInf;
       }
     }
+    // Online softmax with a lazily moved reference point: a row's weights are
+    // exp2((s - m_ref) sc), and m_ref follows the row's running maximum only
+    // when that maximum passes it by more than kRefSlack in the log2 domain,
+    // so a weight stays <= 2^kRefSlack and the accumulators are rescaled on
+    // those tiles alone (a row's first finite scores set it; its
+    // accumulators are still zero then).  The weights are a constant factor
+    // times the ones a reference at the running maximum would give, and their
+    // bf16 rounding is relative, so the result is the same softmax.
     i16x4 pB[MT];
     float alpha[MT];
+    bool moved = false;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       float mx = __builtin_fmaxf(__builtin_fmaxf(sacc[mt][0], sacc[mt][1]), __builtin_fmaxf(sacc[mt][2], sacc[mt][3]));
       mx = row_max4(mx);
-      const float m_new = fmaxf(m_run[mt], mx);
-      const float nb = (m_new == kNegInf) ? 0.f : -m_new * sc;  // exp2 bias
-      alpha[mt] = __builtin_amdgcn_exp2f(fmaf(m_run[mt], sc, nb));
+      const float m_old = m_run[mt];
+      const float m_new = fmaxf(m_old, mx);
+      // (m_old -inf and m_new finite: +inf, a move; both -inf: NaN, none)
+      const bool shift = (m_new - m_old) * sc > kRefSlack;
+      const float m_ref = shift ? m_new : m_old;
+      alpha[mt] = shift ? __builtin_amdgcn_exp2f((m_old - m_new) * sc) : 1.f;
+      moved |= shift && m_old != kNegInf;
+      const float nb = (m_ref == kNegInf) ? 0.f : -m_ref * sc;  // exp2 bias
       float p[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f(fmaf(sacc[mt][i], sc, nb));
       l_run[mt] = fmaf(l_run[mt], alpha[mt], row_sum4((p[0] + p[1]) + (p[2] + p[3])));
-      m_run[mt] = m_new;
+      m_run[mt] = m_ref;
       // P^T as the B operand, rounded to bf16 like the reference's p.to(v.dtype)
       pB[mt] = __builtin_bit_cast(i16x4, make_uint2(pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])));
     }
-    bool moved = false;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) moved |= alpha[mt] != 1.f;
     if (__ballot(moved)) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
