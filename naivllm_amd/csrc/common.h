@@ -38,14 +38,10 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2v){lo, hi}, bf16x2v));
 }
 
-// Round-to-nearest-even narrowing (NaN kept quiet), the rounding torch and
-// the reference's Triton `.to(bfloat16)` apply.
-__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
+// Round-to-nearest-even narrowing (a NaN stays a quiet NaN), the rounding
+// torch and the reference's Triton `.to(bfloat16)` apply: gfx950's
+// conversion instruction, one VALU operation.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) { return (uint16_t)pack_bf16x2(f, 0.f); }
 
 
 // ---------------------------------------------------------------------------

@@ -105,6 +105,38 @@ def test_linear_swiglu(M, I, K, norm):
     torch.testing.assert_close(y.float(), want, **BF16)
 
 
+def bf16_of_magnitudes(g, n, lo_exp, hi_exp):
+    """n bf16 values of random sign, exponent in [lo_exp, hi_exp) and mantissa."""
+    e = torch.randint(lo_exp, hi_exp, (n,), generator=g, device="cuda").float()
+    f = 1.0 + torch.randint(0, 128, (n,), generator=g, device="cuda").float() / 128
+    s = torch.where(torch.rand(n, generator=g, device="cuda") < 0.5, -1.0, 1.0)
+    return (s * f * torch.exp2(e)).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("lo_exp,hi_exp", [(-8, 8), (-110, -100), (118, 128)])
+def test_output_rounding_is_round_to_nearest_even(lo_exp, hi_exp):
+    # y[m][n] = s[n] + t[m] from two unit products: the fp32 sum of two bf16
+    # values (ties, sticky bits and, near the top of the range, overflow to
+    # inf among them) rounded once to bf16, bit for bit as torch rounds the
+    # same fp32 value
+    print(f"case: output rounding exponents [{lo_exp}, {hi_exp})", flush=True)
+    M, N, K = 16, 256, 32
+    g = gen(lo_exp * 131 + hi_exp)
+    s = bf16_of_magnitudes(g, N, lo_exp, hi_exp)
+    t = bf16_of_magnitudes(g, M, lo_exp - 9, hi_exp)  # exponent gaps up to 9 + the range: ties and sticky bits
+    x = torch.zeros(M, K, dtype=torch.bfloat16, device="cuda")
+    x[:, 0] = 1.0
+    x[:, 1] = t
+    w = torch.zeros(N, K, dtype=torch.bfloat16, device="cuda")
+    w[:, 0] = s
+    w[:, 1] = 1.0
+    y = torch.empty(M, N, dtype=torch.bfloat16, device="cuda")
+    qm.linear(x, w, y)
+    want = (s.float().cpu()[None, :] + t.float().cpu()[:, None]).to(torch.bfloat16)
+    got = y.cpu()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16)), (got - want).abs().max()
+
+
 # (4-column tiles: 1, 9, 16, 18 and 31 rows, reductions of whole and partial 128-element chunks, 1-3 per wave)
 @pytest.mark.parametrize("M,N,K", [(9, 1024, 2048), (18, 1024, 3072), (72, 1024, 3072), (100, 256, 512),
                                    (3, 4096, 4096), (1, 1024, 3072), (16, 1024, 1032), (31, 512, 2056)])
