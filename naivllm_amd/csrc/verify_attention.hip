@@ -113,13 +113,13 @@ struct VerifyArgs {
 #define NSV_STAMP_AT(a, slot)                                                                      \
   do {                                                                                             \
     if ((a).stamps && threadIdx.x == 0)                                                            \
-      (a).stamps[blockIdx.x * kStampSlots + (slot)] = __builtin_amdgcn_s_memrealtime();            \
+      (a).stamps[(blockIdx.y * gridDim.x + blockIdx.x) * kStampSlots + (slot)] = __builtin_amdgcn_s_memrealtime();            \
   } while (0)
 // hwreg(HW_REG_XCC_ID = 20, offset 0, 4 bits): the XCD the workgroup runs on
 #define NSV_STAMP_XCC(a)                                                                           \
   do {                                                                                             \
     if ((a).stamps && threadIdx.x == 0)                                                            \
-      (a).stamps[blockIdx.x * kStampSlots + kStampSlots - 1] =                                     \
+      (a).stamps[(blockIdx.y * gridDim.x + blockIdx.x) * kStampSlots + kStampSlots - 1] =                                     \
           (unsigned long long)(__builtin_amdgcn_s_getreg(20 | (3 << 11)) & 15);                    \
   } while (0)
 #else
@@ -197,6 +197,23 @@ __device__ __forceinline__ int num_splits(const VerifyArgs& a, int ctx) {
   const int len = split_len(a, ctx);
   return ctx <= len ? 1 : (ctx + len - 1) / len;
 }
+
+// n / d for 0 <= n < 2^22 and d >= 1 through an fp32 reciprocal (relative
+// error ~2^-22, so the truncated estimate is the quotient or one below it)
+// and one correction: a few instructions where the integer division
+// sequence is ~25, on the key-split kernel's path to its first loads.
+__device__ __forceinline__ int div_small(int n, int d) {
+  int q = (int)((float)n * __builtin_amdgcn_rcpf((float)d));
+  const int r = n - q * d;
+  q += (r >= d) - (r < 0);
+  return q;
+}
+__device__ __forceinline__ int split_len_ks(const VerifyArgs& a, int ctx) {
+  if (a.split_tokens > 0) return a.split_tokens;
+  const int per = div_small(ctx + a.ks_splits - 1, a.ks_splits);
+  return per <= 16 ? 16 : (per + 15) & ~15;
+}
+__device__ __forceinline__ int num_splits_ks(int ctx, int len) { return ctx <= len ? 1 : div_small(ctx + len - 1, len); }
 
 // Workgroup -> (split, pair) with every split of a (sequence, kv-head) pair
 // on the same XCD (workgroups are dealt to the 8 XCDs round-robin), so the
@@ -904,14 +921,13 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
   unsigned char* const q_lds = lds.q_lds;
   unsigned char* const smem = lds.smem;
 
-  // ---- workgroup -> (pair, split); every split of a pair on one XCD
-  const int wg = blockIdx.x;
-  const int yy = wg >> 3;
+  // ---- workgroup -> (pair, split): grid (8 P8, splits), so workgroup
+  // y * 8 P8 + x runs on XCD x % 8 -- every split of a pair on one XCD
   fetch_args(a);
   NSV_STAMP_AT(a, 0);  // entry
   NSV_STAMP_XCC(a);
-  const int pair_raw = (yy % a.P8) * 8 + (wg & 7);
-  const int split = yy / a.P8;
+  const int pair_raw = blockIdx.x;
+  const int split = blockIdx.y;
   // (the grid rounds the pair count up to a multiple of 8: workgroups past
   // the last pair read its metadata and leave once it is back -- an exit
   // before those loads would put the kernel arguments the loads need into a
@@ -920,7 +936,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g4 = lane >> 4, c = lane & 15;
-  const int b = pair / a.Hkv, hk = pair - b * a.Hkv;
+  const int b = div_small(pair, a.Hkv), hk = pair - b * a.Hkv;
 
   // ---- first round trip: block-table row, context length, query range, all
   // issued before any is used (entries past the row read its last one and
@@ -937,9 +953,9 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
   if (pair_raw >= a.npairs) return;
   const int ctx = clamp_context(a, ctx_raw);
   const int qlen = q1 - q0;
-  const int nsplit = num_splits(a, ctx);
+  const int len = split_len_ks(a, ctx);
+  const int nsplit = num_splits_ks(ctx, len);
   if (split >= nsplit || qlen < 0) return;  // uniform per workgroup
-  const int len = split_len(a, ctx);
   const int kb = split * len;
   const int ke = min(ctx, kb + len);
 #pragma unroll
@@ -1792,7 +1808,8 @@ int make_plan(int B, int H, int Hkv, int D, int block_size, int max_blocks, int 
   // of query rows (decode-shaped calls: at 8 pairs x 1.25k keys and 2 or 4
   // rows per pair, 8.0 us against 9.4 for the d-sliced kernel and its merge).
   const int64_t ks_slots = (int64_t)cus * (8 / kKsWaves);  // resident workgroups
-  const bool ks_fits = p->MT <= 3 && block_size >= 16 && max_blocks <= kMaxSplitPages &&
+  // (contexts under 2^22 keys: the kernel's split arithmetic, div_small)
+  const bool ks_fits = p->MT <= 3 && block_size >= 16 && max_blocks <= kMaxSplitPages && max_ctx < (1 << 22) &&
                        (pairs <= kMaxCounterPairs || (kv_split_tokens == 0 && pairs >= ks_slots));
   const bool ks_wins = kv_split_tokens > 0 || pairs * 16 >= ks_slots || max_ctx >= 4096 || p->MT == 1;
   if (dtype == NSV_BF16 && ks_fits && ks_wins) {
@@ -2049,10 +2066,11 @@ int launch_verify(const VerifyArgs& a, const Plan& p, int D, int dtype, hipStrea
   int rc = NSV_OK;
   const dim3 grid(8 * p.S * a.P8 * p.dqc);
   if (dtype == NSV_BF16 && p.ks) {
+    const dim3 kgrid(8 * a.P8, p.S);  // (pair, split)
     switch (p.MT) {
-      case 1: rc = launch_ks<1>(a, D, grid, s); break;
-      case 2: rc = launch_ks<2>(a, D, grid, s); break;
-      default: rc = launch_ks<3>(a, D, grid, s); break;
+      case 1: rc = launch_ks<1>(a, D, kgrid, s); break;
+      case 2: rc = launch_ks<2>(a, D, kgrid, s); break;
+      default: rc = launch_ks<3>(a, D, kgrid, s); break;
     }
     if (rc != NSV_OK) return rc;
   } else if (dtype == NSV_BF16) {
