@@ -199,9 +199,9 @@ __device__ __forceinline__ int num_splits(const VerifyArgs& a, int ctx) {
 }
 
 // n / d for 0 <= n < 2^22 and d >= 1 through an fp32 reciprocal (relative
-// error ~2^-22, so the truncated estimate is the quotient or one below it)
-// and one correction: a few instructions where the integer division
-// sequence is ~25, on the key-split kernel's path to its first loads.
+// error ~2^-22, so the truncated estimate is within one of the quotient) and
+// one correction: a few instructions where the integer division sequence is
+// ~25, on the attention kernels' paths to their first loads.
 __device__ __forceinline__ int div_small(int n, int d) {
   int q = (int)((float)n * __builtin_amdgcn_rcpf((float)d));
   const int r = n - q * d;
@@ -333,13 +333,12 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
   unsigned char* const smem = lds.smem;
   float* const park = lds.park;
 
-  // ---- workgroup -> (pair, dq, split); every workgroup of a pair on one XCD
-  const int wg = blockIdx.x;
-  const int yy = wg >> 3;
+  // ---- workgroup -> (pair, dq, split): grid (8 P8, dqc, splits), so
+  // workgroup (z dqc + y) 8 P8 + x runs on XCD x % 8 -- every workgroup of a
+  // pair on one XCD
   fetch_args(a);
-  const int pair_raw = (yy % a.P8) * 8 + (wg & 7);
-  const int rest = yy / a.P8;
-  const int dq = rest % a.dqc, split = rest / a.dqc;
+  const int pair_raw = blockIdx.x;
+  const int dq = blockIdx.y, split = blockIdx.z;
   // (the grid rounds the pair count up to a multiple of 8: workgroups past
   // the last pair, or past the table's keys, read clamped metadata and leave
   // once it is back -- an exit before those loads would put the kernel
@@ -348,7 +347,7 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g4 = lane >> 4, c = lane & 15;
-  const int b = pair / a.Hkv, hk = pair - b * a.Hkv;
+  const int b = div_small(pair, a.Hkv), hk = pair - b * a.Hkv;
   const int max_ctx = a.max_blocks << a.bs_log2;
   const int tok_begin = split * a.split_tokens;
   const int range_end = min(max_ctx, tok_begin + a.split_tokens);
@@ -386,7 +385,7 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int m = mt * 16 + c;
-      const int g = m / a.QL, t = m - g * a.QL;
+      const int g = div_small(m, a.QL), t = m - g * a.QL;
       const bool ok = (m < a.Mv) && (t < qlen);
       const int row = ok ? q0 + t : 0;
       const int gg = ok ? g : 0;
@@ -400,7 +399,7 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int m = mt * 16 + c;
-      const int g = m / a.QL, t = m - g * a.QL;
+      const int g = div_small(m, a.QL), t = m - g * a.QL;
       const bool ok = (m < a.Mv) && (t < qlen);
       qpos[mt] = ok ? qpos[mt] : -1;
       if (qpos[mt] >= 0) qmin = min(qmin, qpos[mt]);
@@ -686,7 +685,7 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
       const int qd = tid + j * NT;
       int m = qd / C4;
       const int c4 = qd - m * C4;
-      const int g = m / a.QL, t = m - g * a.QL;
+      const int g = div_small(m, a.QL), t = m - g * a.QL;
       const bool ok = m < a.Mv && t < qlen;
       iok[j] = ok;
       m = ok ? m : 0;  // (items past the rows load row 0 and are discarded)
@@ -757,7 +756,7 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
         o += f * *reinterpret_cast<const f32x4*>(&park[(ww * MP + m) * RSTR + c4 * 4]);
       }
       if (nsplit == 1) {
-        const int g = m / a.QL, t = m - g * a.QL;
+        const int g = div_small(m, a.QL), t = m - g * a.QL;
         if (t >= qlen) continue;
         const float inv = (L > 0.f && row_pos[m] >= 0) ? 1.f / L : 0.f;
         bf16_t* dst = (bf16_t*)a.out + ((int64_t)(q0 + t) * a.H + hk * a.Gs + a.g0 + g) * DH + dq * DC + c4 * 4;
@@ -825,7 +824,7 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
 #pragma unroll
       for (int ww = 1; ww < NW; ++ww) o += *reinterpret_cast<const f32x4*>(&region[(ww * MTP * 16 + r) * RSTR + c4 * 4]);
       if (nsplit == 1) {
-        const int g = m / a.QL, t = m - g * a.QL;
+        const int g = div_small(m, a.QL), t = m - g * a.QL;
         if (t >= qlen) continue;
         const float L = row_l[m];
         const float inv = (L > 0.f && row_pos[m] >= 0) ? 1.f / L : 0.f;
@@ -972,7 +971,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int m = mt * 16 + c;
-      const int g = m / a.QL, t = m - g * a.QL;
+      const int g = div_small(m, a.QL), t = m - g * a.QL;
       const bool ok = (m < a.Mv) && (t < qlen);
       qpos[mt] = load_pos(a.positions, ok ? q0 + t : 0);
     }
@@ -981,7 +980,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
     for (int i = 0; i < QPASS; ++i) {
       const int idx = tid + i * NT;
       const int m = idx / VCH, ch = idx % VCH;
-      const int g = m / a.QL, t = m - g * a.QL;
+      const int g = div_small(m, a.QL), t = m - g * a.QL;
       const bool ok = (idx < MP * VCH) && (m < a.Mv) && (t < qlen);
       const int row = ok ? q0 + t : 0;
       const int gg = ok ? g : 0;
@@ -1000,7 +999,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int m = mt * 16 + c;
-      const int g = m / a.QL, t = m - g * a.QL;
+      const int g = div_small(m, a.QL), t = m - g * a.QL;
       const bool ok = (m < a.Mv) && (t < qlen);
       qpos[mt] = ok ? qpos[mt] : -1;
       if (qpos[mt] >= 0) qmin = min(qmin, qpos[mt]);
@@ -1295,7 +1294,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
       if (row_pos[m] < 0) o = f32x4{0.f, 0.f, 0.f, 0.f};
       own[ps][j] = o;
       if (nsplit == 1) {
-        const int g = m / a.QL, t = m - g * a.QL;
+        const int g = div_small(m, a.QL), t = m - g * a.QL;
         if (t >= qlen) continue;
         const float L = row_l[m];
         const float inv = L > 0.f ? 1.f / L : 0.f;
@@ -1333,7 +1332,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
       const int qd = tid + j * NT;
       const int r = qd / C4, c4 = qd % C4;
       int m = ps * MROWS + r;
-      const int g = m / a.QL, t = m - g * a.QL;
+      const int g = div_small(m, a.QL), t = m - g * a.QL;
       const bool ok = r < MROWS && m < a.Mv && t < qlen;
       iok[ps][j] = ok;
       m = ok ? m : 0;
@@ -2074,11 +2073,12 @@ int launch_verify(const VerifyArgs& a, const Plan& p, int D, int dtype, hipStrea
     }
     if (rc != NSV_OK) return rc;
   } else if (dtype == NSV_BF16) {
+    const dim3 dgrid(8 * a.P8, p.dqc, p.S);  // (pair, head-dim slice, split)
     switch (p.MT) {
-      case 1: rc = launch_bf16<1>(a, D, grid, s); break;
-      case 2: rc = launch_bf16<2>(a, D, grid, s); break;
-      case 3: rc = launch_bf16<3>(a, D, grid, s); break;
-      default: rc = launch_bf16<4>(a, D, grid, s); break;
+      case 1: rc = launch_bf16<1>(a, D, dgrid, s); break;
+      case 2: rc = launch_bf16<2>(a, D, dgrid, s); break;
+      case 3: rc = launch_bf16<3>(a, D, dgrid, s); break;
+      default: rc = launch_bf16<4>(a, D, dgrid, s); break;
     }
     if (rc != NSV_OK) return rc;
   } else {
