@@ -23,6 +23,17 @@ __device__ __forceinline__ u32x4 load16_stream(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
 }
 
+// n / d for 0 <= n < 2^22 and d >= 1 through an fp32 reciprocal (relative
+// error ~2^-22, so the truncated estimate is within one of the quotient) and
+// one correction: a few instructions where the integer division sequence is
+// ~25, on the attention kernels' paths to their first loads.
+__device__ __forceinline__ int div_small(int n, int d) {
+  int q = (int)((float)n * __builtin_amdgcn_rcpf((float)d));
+  const int r = n - q * d;
+  q += (r >= d) - (r < 0);
+  return q;
+}
+
 // Raw 16-bit pattern of a bf16 value and back; bf16 is the upper half of an
 // IEEE-754 binary32, so widening is a shift.
 __device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {

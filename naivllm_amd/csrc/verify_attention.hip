@@ -198,16 +198,6 @@ __device__ __forceinline__ int num_splits(const VerifyArgs& a, int ctx) {
   return ctx <= len ? 1 : (ctx + len - 1) / len;
 }
 
-// n / d for 0 <= n < 2^22 and d >= 1 through an fp32 reciprocal (relative
-// error ~2^-22, so the truncated estimate is within one of the quotient) and
-// one correction: a few instructions where the integer division sequence is
-// ~25, on the attention kernels' paths to their first loads.
-__device__ __forceinline__ int div_small(int n, int d) {
-  int q = (int)((float)n * __builtin_amdgcn_rcpf((float)d));
-  const int r = n - q * d;
-  q += (r >= d) - (r < 0);
-  return q;
-}
 __device__ __forceinline__ int split_len_ks(const VerifyArgs& a, int ctx) {
   if (a.split_tokens > 0) return a.split_tokens;
   const int per = div_small(ctx + a.ks_splits - 1, a.ks_splits);
