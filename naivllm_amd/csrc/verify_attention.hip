@@ -113,13 +113,13 @@ struct VerifyArgs {
 #define NSV_STAMP_AT(a, slot)                                                                      \
   do {                                                                                             \
     if ((a).stamps && threadIdx.x == 0)                                                            \
-      (a).stamps[(blockIdx.y * gridDim.x + blockIdx.x) * kStampSlots + (slot)] = __builtin_amdgcn_s_memrealtime();            \
+      (a).stamps[((blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * kStampSlots + (slot)] = __builtin_amdgcn_s_memrealtime();            \
   } while (0)
 // hwreg(HW_REG_XCC_ID = 20, offset 0, 4 bits): the XCD the workgroup runs on
 #define NSV_STAMP_XCC(a)                                                                           \
   do {                                                                                             \
     if ((a).stamps && threadIdx.x == 0)                                                            \
-      (a).stamps[(blockIdx.y * gridDim.x + blockIdx.x) * kStampSlots + kStampSlots - 1] =                                     \
+      (a).stamps[((blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x) * kStampSlots + kStampSlots - 1] =                                     \
           (unsigned long long)(__builtin_amdgcn_s_getreg(20 | (3 << 11)) & 15);                    \
   } while (0)
 #else
@@ -327,6 +327,8 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
   // workgroup (z dqc + y) 8 P8 + x runs on XCD x % 8 -- every workgroup of a
   // pair on one XCD
   fetch_args(a);
+  NSV_STAMP_AT(a, 0);  // entry
+  NSV_STAMP_XCC(a);
   const int pair_raw = blockIdx.x;
   const int dq = blockIdx.y, split = blockIdx.z;
   // (the grid rounds the pair count up to a multiple of 8: workgroups past
@@ -361,6 +363,7 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
   const int qlen = q1 - q0;
   const int nsplit = num_splits(a, ctx);
   if (split >= nsplit || qlen < 0) return;  // uniform per workgroup
+  NSV_STAMP_AT(a, 1);  // metadata back
   const int tok_end = min(ctx, range_end);
 #pragma unroll
   for (int i = 0; i < PPT; ++i) {
@@ -433,10 +436,10 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
   };
 
   // Issue every load of wave-tile `it`.  Masked keys read the row of a key
-  // that exists (finite data, zero weight), or any mapped row when none does.
-  // Tiles past the split's end have no key and read the pool's first row
-  // (one cached line): every issue has the same loads, so the compiler's
-  // wait counts stay exact across the pipeline.
+  // that exists (finite data, zero weight).  A tile without any key (past
+  // the split's end, or on an unmapped page) issues no load: such dummy
+  // loads, a few per wave at these short splits, queued behind the real
+  // tiles in the CU's address unit (b1: ~1.5 us before the waves merged).
   auto issue = [&](Tile& T, int it) {
     T.n0 = tok_begin + (it * NW + w) * kTile;
     if constexpr (UPAGE) {
@@ -446,6 +449,7 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
       if (pg < 0) nvalid = 0;
       T.nvalid = nvalid;
       T.kmask = nvalid >= kTile ? 0xffffffffull : ((1ull << nvalid) - 1);
+      if (nvalid == 0) return;  // uniform
       // byte addressing: scalar page base + 32-bit lane offsets
       const size_t page_off = (size_t)(pg < 0 ? 0 : pg) * (size_t)page_elems * 2;
       const char* kp = (const char*)kbase + page_off;
@@ -472,6 +476,7 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
       const int pg = (lane < kTile && n < tok_end) ? pages[(n >> a.bs_log2) - pg0] : -1;
       T.kmask = __ballot(pg >= 0);
       T.nvalid = 0;
+      if (T.kmask == 0) return;  // uniform
       const int first = T.kmask ? __builtin_ctzll(T.kmask) : 0;
       const int pg_first = __shfl(pg, first, NSV_WAVE);
       const int64_t dflt = T.kmask ? (int64_t)pg_first * page_elems + (int64_t)((T.n0 + first) & bs_mask) * tok_stride
@@ -628,9 +633,11 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
     for (int s = 0; s < NS; ++s) {
       __builtin_amdgcn_sched_barrier(0);
       compute(T[s]);
+      if (it == 0 && s == 0) NSV_STAMP_AT(a, 2);  // first tile computed
       issue(T[s], it + s + NS);
     }
   }
+  NSV_STAMP_AT(a, 3);  // key loop done (wave 0)
 
   // ---- merge the waves' (max, sum, O) ---------------------------------------
   if (g4 == 0) {
@@ -657,6 +664,7 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
       ds_last = __hip_atomic_fetch_add(&a.counters[slot], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                 (unsigned)(nsplit - 1);
     __syncthreads();
+    NSV_STAMP_AT(a, 5);  // arrival counted
     if (!uniform(ds_last)) return;
     if (tid == 0) __hip_atomic_store(&a.counters[slot], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int64_t base0 = (int64_t)pair * a.S * a.Mv;  // row 0 of split 0
@@ -721,6 +729,7 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
       const uint32_t hi = pack_bf16x2(num[j][2] * inv, num[j][3] * inv);
       *idst[j] = make_uint2(lo, hi);
     }
+    NSV_STAMP_AT(a, 6);  // merge stores issued (last split)
   };
   if constexpr (PARK) {
     // lane (g4, c) element i of tile (dt, mt) is O[16*mt + c][16*dt + 4*g4 + i]
@@ -730,6 +739,7 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
       for (int dt = 0; dt < DT; ++dt)
         *reinterpret_cast<f32x4*>(&park[(w * MP + mt * 16 + c) * RSTR + dt * 16 + g4 * 4]) = acc[dt][mt];
     __syncthreads();
+    NSV_STAMP_AT(a, 7);  // every wave's key loop done, O parked
     constexpr int C4 = DC / 4;
     for (int qd = tid; qd < a.Mv * C4; qd += NT) {
       const int m = qd / C4, c4 = qd - m * C4;
@@ -769,6 +779,7 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
       store_agent(reinterpret_cast<uint64_t*>(&a.part_ml[(pbase + tid) * 2]),
                   row_pos[tid] >= 0 && M != kNegInf ? M * sc : kNegInf, row_pos[tid] >= 0 ? L : 0.f);
     }
+    NSV_STAMP_AT(a, 4);  // waves merged, partials issued
     if (nsplit > 1 && a.dmerge) merge_splits();
     return;
   }
@@ -1035,7 +1046,8 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
   // start on 16-key boundaries and pages hold a power of two >= 16 keys).
   // Missing keys, and tiles past the split, read a row that exists or the
   // pool's first row: every issue has the same loads, so the compiler's
-  // wait counts stay exact across the pipeline.
+  // wait counts stay exact across the pipeline.  (Skipping the loads of
+  // tiles without keys measured slower here: config 2 13.6 -> 14.4 us.)
   auto issue = [&](Tile& T, int it) {
     T.n0 = kb + (it * NW + w) * TK;
     int nvalid = min(max(ke - T.n0, 0), TK);
