@@ -1044,17 +1044,22 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
 
   // Issue every load of wave-tile `it` (tiles never cross a page: splits
   // start on 16-key boundaries and pages hold a power of two >= 16 keys).
-  // Missing keys, and tiles past the split, read a row that exists or the
-  // pool's first row: every issue has the same loads, so the compiler's
-  // wait counts stay exact across the pipeline.  (Skipping the loads of
-  // tiles without keys measured slower here: config 2 13.6 -> 14.4 us.)
-  auto issue = [&](Tile& T, int it) {
+  // Missing keys read a row that exists.  A wave's first tile is always
+  // issued (a tile past the split reads the pool's first row), so the
+  // compiler's wait for the query rows staged before the first barrier
+  // stays exact and that barrier does not wait for the tile; a later tile
+  // without any key issues no load (the loop waits for vmcnt(0) anyway),
+  // so no dummy loads queue in the CU's address unit beside real tiles.
+  auto issue = [&](Tile& T, int it, auto skip_empty) {
     T.n0 = kb + (it * NW + w) * TK;
     int nvalid = min(max(ke - T.n0, 0), TK);
     int pg = nvalid > 0 ? pages[T.n0 >> a.bs_log2] : -1;
     pg = __builtin_amdgcn_readfirstlane(pg);
     if (pg < 0) nvalid = 0;
     T.nvalid = nvalid;
+    if constexpr (decltype(skip_empty)::value) {
+      if (nvalid == 0) return;  // uniform
+    }
     const size_t page_off = (size_t)(pg < 0 ? 0 : pg) * page_bytes;
     const char* kp = kbase + page_off;
     const char* vp = vbase + page_off;
@@ -1185,7 +1190,7 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
   load_q();
   Tile T0, T1;
   __builtin_amdgcn_sched_barrier(0);
-  issue(T0, 0);
+  issue(T0, 0, std::false_type{});
   __builtin_amdgcn_sched_barrier(0);
   finish_positions();
   store_q();
@@ -1194,13 +1199,13 @@ __global__ __launch_bounds__(NW * 64, 8 / NW) void verify_attn_ks_kernel(VerifyA
     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): tile it landed
     __builtin_amdgcn_sched_barrier(0);
     if (it == 0) NSV_STAMP_AT(a, 2);  // first tile landed
-    if (it + 1 < niter) issue(T1, it + 1);
+    if (it + 1 < niter) issue(T1, it + 1, std::true_type{});
     __builtin_amdgcn_sched_barrier(0);
     compute(T0);
     if (it + 1 >= niter) break;
     __builtin_amdgcn_s_waitcnt(0x0f70);  // vmcnt(0): tile it + 1 landed
     __builtin_amdgcn_sched_barrier(0);
-    if (it + 2 < niter) issue(T0, it + 2);
+    if (it + 2 < niter) issue(T0, it + 2, std::true_type{});
     __builtin_amdgcn_sched_barrier(0);
     compute(T1);
   }
