@@ -51,14 +51,14 @@ def algorithmic_flops(ctx_lens, q_rows_per_seq, H, D) -> int:
 
 
 class Workload:
-    def __init__(self, config: int, layers: int, seed: int, device):
+    def __init__(self, config: int, layers: int, seed: int, device, batch: int = 8):
         self.config = config
         if config == 2:
-            self.B, self.H, self.Hkv, self.D, self.bs, self.K = 8, 16, 8, 128, 256, 8
+            self.B, self.H, self.Hkv, self.D, self.bs, self.K = batch, 16, 8, 128, 256, 8
             self.ctx = synth.config2_ctx_lens(seed, self.B)
             self.layers = layers
-            pool_pages = 64
-            name = "verify-attention, Qwen3-0.6B layer shape, b8 bf16, L~U[1200,1300], K=8, 28 layers"
+            pool_pages = max(64, sum((c + self.bs - 1) // self.bs for c in self.ctx))
+            name = f"verify-attention, Qwen3-0.6B layer shape, b{batch} bf16, L~U[1200,1300], K=8, 28 layers"
         elif config == 4:
             self.B, self.H, self.Hkv, self.D, self.bs, self.K = 16, 32, 8, 128, 256, 8
             self.ctx = [int(x) for x in synth.randint(seed, 7, 16, 16384, 32769)]
@@ -671,6 +671,8 @@ def main():
                     help="load libnaivspec_stamp.so, print the kernel's per-workgroup timeline of the workload "
                          "(medians over workgroups, graph-replayed like the metric) and exit")
     ap.add_argument("--seed", type=int, default=2)
+    ap.add_argument("--batch", type=int, default=8,
+                    help="sequences of the config-2 workload for --stamps and --ceiling (1: the b1 round's attention shape)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
                     help="run only a plain device copy of this many MiB (calibrates rocprofv3's "
                          "FETCH_SIZE / WRITE_SIZE counters against a known byte count) and exit")
@@ -678,6 +680,10 @@ def main():
     if args.copy_probe_mib > 0:
         copy_probe(args.copy_probe_mib)
         return
+    if args.batch != 8 and not (args.stamps or args.ceiling):
+        raise SystemExit("--batch applies to --stamps and --ceiling only (the metric is quoted at b8)")
+    if not 1 <= args.batch <= 64:
+        raise SystemExit("--batch must be in [1, 64]")
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus})",
               file=sys.stderr)
@@ -691,7 +697,7 @@ def main():
     if args.accept:
         print(json.dumps({"rejection_sampling": rejection_sampling()}), flush=True)
         return
-    wl = Workload(args.config, args.layers, args.seed, dev)
+    wl = Workload(args.config, args.layers, args.seed, dev, batch=args.batch)
     print(f"[bench] workload: {wl.name}; ctx={wl.ctx}", file=sys.stderr, flush=True)
     if args.ceiling:
         print(json.dumps({"ceiling": ceilings(wl)}), flush=True)
