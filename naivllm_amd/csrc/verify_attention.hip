@@ -14,7 +14,9 @@
 //     products); V is staged through LDS and read back with gfx950's
 //     transposing LDS read;
 //   * every K/V load of a tile is unconditional (missing keys read a mapped
-//     row), so the compiler's wait counts stay exact across the pipeline.
+//     row), so the compiler's wait counts stay exact across the pipeline; a
+//     tile with no key at all issues no load (in the key-split kernel from a
+//     wave's second tile on), so no dummy loads queue beside real ones.
 //
 // Two bf16 decompositions, chosen by make_plan:
 //   * key-split (verify_attn_ks_kernel): workgroup = (pair, key split), full
