@@ -415,6 +415,38 @@ def ceilings(wl: "Workload") -> dict:
             "stream_us": round(stream_us, 3), "stream_GBs": round(kv_bytes / stream_us / 1e3, 1)}
 
 
+def cu_intake(per_mib=(1,), groups=(32, 64, 128, 256)) -> dict:
+    """How fast a few CUs take in bytes, against the whole chip: G
+    workgroups of 512 threads each read their own contiguous per-MiB slice
+    (nsv_stream_read, 16-byte non-temporal loads), graph-replayed over 8
+    rotating slices of a 2 GiB buffer so that every call reads from HBM.
+    Reported per G: us per call, total GB/s and GB/s per workgroup (one
+    workgroup per CU at these counts)."""
+    from naivllm_amd import _lib
+
+    h = _lib.lib()
+    dev = torch.device("cuda:0")
+    buf = torch.ones(2 << 30, dtype=torch.uint8, device=dev)
+    sink = torch.zeros(65536, dtype=torch.int32, device=dev)
+    out = {}
+    for mib in per_mib:
+        for g in groups:
+            nbytes = g * (mib << 20)
+            slots = min(8, (2 << 30) // nbytes)
+
+            def step():
+                s = torch.cuda.current_stream().cuda_stream
+                for i in range(8):
+                    off = (i % slots) * nbytes
+                    _lib.check(h.nsv_stream_read(buf.data_ptr() + off, nbytes, g, sink.data_ptr(), s), "stream")
+            us = _graph_us(step, 8, steps=20)
+            out[f"{g}x{mib}MiB"] = {"us": round(us, 2), "GBs": round(nbytes / us / 1e3, 1),
+                                    "GBs_per_workgroup": round(nbytes / g / us / 1e3, 1)}
+    del buf
+    torch.cuda.empty_cache()
+    return out
+
+
 STAMP_POINTS = ["entry", "metadata back", "first tile landed", "key loop done (wave 0)", "waves merged",
                 "arrival counted", "split merge done", "every wave's key loop done", "O rows in LDS"]
 
@@ -671,6 +703,8 @@ def main():
                     help="load libnaivspec_stamp.so, print the kernel's per-workgroup timeline of the workload "
                          "(medians over workgroups, graph-replayed like the metric) and exit")
     ap.add_argument("--seed", type=int, default=2)
+    ap.add_argument("--cu-intake", action="store_true",
+                    help="time contiguous reads by 32-256 workgroups (one per CU): per-CU against chip-wide intake, and exit")
     ap.add_argument("--batch", type=int, default=8,
                     help="sequences of the config-2 workload for --stamps and --ceiling (1: the b1 round's attention shape)")
     ap.add_argument("--copy-probe-mib", type=int, default=0,
@@ -696,6 +730,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.accept:
         print(json.dumps({"rejection_sampling": rejection_sampling()}), flush=True)
+        return
+    if args.cu_intake:
+        print(json.dumps({"cu_intake": cu_intake()}), flush=True)
         return
     wl = Workload(args.config, args.layers, args.seed, dev, batch=args.batch)
     print(f"[bench] workload: {wl.name}; ctx={wl.ctx}", file=sys.stderr, flush=True)
