@@ -421,7 +421,8 @@ def cu_intake(per_mib=(1,), groups=(32, 64, 128, 256)) -> dict:
     (nsv_stream_read, 16-byte non-temporal loads), graph-replayed over 8
     rotating slices of a 2 GiB buffer so that every call reads from HBM.
     Reported per G: us per call, total GB/s and GB/s per workgroup (one
-    workgroup per CU at these counts)."""
+    workgroup per CU at these counts); and the time per call of a graph of
+    64 one-workgroup, one-load kernels (the floor of a dependent launch)."""
     from naivllm_amd import _lib
 
     h = _lib.lib()
@@ -442,6 +443,13 @@ def cu_intake(per_mib=(1,), groups=(32, 64, 128, 256)) -> dict:
             us = _graph_us(step, 8, steps=20)
             out[f"{g}x{mib}MiB"] = {"us": round(us, 2), "GBs": round(nbytes / us / 1e3, 1),
                                     "GBs_per_workgroup": round(nbytes / g / us / 1e3, 1)}
+
+    # the floor of one dependent launch in a graph: one workgroup, one 16-byte load
+    def tiny():
+        s = torch.cuda.current_stream().cuda_stream
+        for i in range(64):
+            _lib.check(h.nsv_stream_read(buf.data_ptr() + i * 4096, 16, 1, sink.data_ptr(), s), "stream")
+    out["one_load_kernel_us"] = round(_graph_us(tiny, 64, steps=20), 2)
     del buf
     torch.cuda.empty_cache()
     return out
