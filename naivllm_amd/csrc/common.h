@@ -167,6 +167,8 @@ __device__ __forceinline__ void head_norm_rope(float x1, float x2, float inv, fl
 // atomics.  Nothing needs them single-copy atomic where readers load only
 // after every writer's stores were acknowledged (the in-kernel merges).
 constexpr int kCpolSc1 = 16;
+// the non-temporal policy of a buffer load (as load16_stream's)
+constexpr int kCpolNt = 2;
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t block_rsrc(const void* base) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, 0x7fffffff, 0x00020000);
 }

@@ -668,11 +668,20 @@ __global__ __launch_bounds__(kStreamWaves * 64, 1) void stream_linear_kernel(Str
   __syncthreads();
   if (my_tiles == 0) return;
 
-  // weight rows of this wave's tile i (past its last tile: the last again, read and never multiplied)
-  auto wrow = [&](int i) { return a.w + ((int64_t)(gw + min(i, my_tiles - 1) * nwaves) * 16 + c) * K + 8 * g4; };
-  auto issue = [&](u32x4 (&buf)[8], const uint16_t* p) {
+  // The weights through a buffer resource of exactly N x K elements (the
+  // plan admits this kernel only a MiB below 2^31 bytes).  wrow(i): byte offset
+  // of this lane's row of the wave's tile i; past its last tile the offset
+  // lies at the resource's end, so the group the loop issues ahead after
+  // the last tile returns zeros without a memory access (it used to re-read
+  // the last tile, and the wave's end waited for those loads).
+  const __amdgpu_buffer_rsrc_t wrs =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.w), (short)0, (int)((int64_t)a.N * K * 2), 0x00020000);
+  const int w_end = (int)((int64_t)a.N * K * 2);
+  auto wrow = [&](int i) { return i < my_tiles ? ((((gw + i * nwaves) * 16 + c) * K) + 8 * g4) * 2 : w_end; };
+  auto issue = [&](u32x4 (&buf)[8], int off) {
 #pragma unroll
-    for (int s = 0; s < 8; ++s) buf[s] = load16_stream(p + 32 * s);
+    for (int s = 0; s < 8; ++s)
+      buf[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, off + 64 * s, 0, kCpolNt));
   };
   f32x4 acc[MT];
 #pragma unroll
@@ -698,19 +707,19 @@ __global__ __launch_bounds__(kStreamWaves * 64, 1) void stream_linear_kernel(Str
   u32x4 A[8], B[8];
   issue(A, wrow(0));
   for (int i = 0; i < my_tiles; ++i) {
-    const uint16_t* p = wrow(i);
-    const uint16_t* pn = wrow(i + 1);
+    const int p = wrow(i);
+    const int pn = wrow(i + 1);
     // (scheduling barriers keep each group's 8 loads together and after the
     // multiplies that free their registers: the compiler otherwise spreads
     // them between the multiplies, reusing registers of loads in flight)
 #pragma unroll
     for (int kg = 0; kg < NG; kg += 2) {
       __builtin_amdgcn_sched_barrier(0);
-      issue(B, p + (kg + 1) * kStreamKG);
+      issue(B, p + (kg + 1) * kStreamKG * 2);
       __builtin_amdgcn_sched_barrier(0);
       compute(A, kg);
       __builtin_amdgcn_sched_barrier(0);
-      issue(A, kg + 2 < NG ? p + (kg + 2) * kStreamKG : pn);
+      issue(A, kg + 2 < NG ? p + (kg + 2) * kStreamKG * 2 : pn);
       __builtin_amdgcn_sched_barrier(0);
       compute(B, kg + 1);
     }
@@ -726,7 +735,7 @@ __global__ __launch_bounds__(kStreamWaves * 64, 1) void stream_linear_kernel(Str
       acc[mt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
   }
-  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last (unused) group's loads
+  __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the last (unused, out-of-range) group's loads
 }
 
 // Streaming kernel for a wide plain projection: at least four 16-row weight
@@ -735,7 +744,8 @@ __global__ __launch_bounds__(kStreamWaves * 64, 1) void stream_linear_kernel(Str
 bool stream_wide(int M, int N, int K, bool norm, int epi, int cus) {
   return !norm && epi == 0 && M >= 1 && M <= kMaxRows && (K == 1024 || K == 2048 || K == 4096) &&
          (int64_t)(N / kBN) >= 32LL * cus && (int64_t)M * (K + 8) * 2 <= kStreamLds &&
-         (int64_t)M * N * 2 < ((int64_t)1 << 31);
+         (int64_t)M * N * 2 < ((int64_t)1 << 31) &&
+         (int64_t)N * K * 2 <= ((int64_t)1 << 31) - (1 << 20);  // weight byte offsets (and one group past the end) fit an int
 }
 
 template <int MT, int NG>
