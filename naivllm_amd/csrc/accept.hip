@@ -76,10 +76,11 @@ __device__ __forceinline__ float round_dt_d(double x, int dtype) { return round_
 // (hipcc keeps fp32 division correctly rounded: -fhip-fp32-correctly-rounded-divide-sqrt is its default)
 __device__ __forceinline__ float div_dt(float a, float b, int dtype) { return round_dt(a / b, dtype); }
 
-// the fp64 exp table, copied into LDS by a workgroup's first 64 threads
-// (visible after the workgroup's next barrier)
+// the fp64 exp table, copied into LDS by a workgroup's 256 threads, one
+// entry each (visible after the workgroup's next barrier)
+static_assert(kThreads >= 256, "one thread per exp table entry");
 __device__ __forceinline__ void load_exp_table(double* tab) {
-  if (threadIdx.x < 64) tab[threadIdx.x] = kExp2Frac64[threadIdx.x];
+  if (threadIdx.x < 256) tab[threadIdx.x] = kExp2Frac256[threadIdx.x];
 }
 
 // softmax value of one element: exp(z - m) * (1 / s) in fp64 (within a few
@@ -396,7 +397,7 @@ __global__ __launch_bounds__(kThreads) void stoch_stats_kernel(StochArgs a) {
   __shared__ float redf[kWaves];
   __shared__ double redd[kWaves];
   __shared__ uint64_t redk[kWaves];
-  __shared__ double etab[64];
+  __shared__ double etab[256];
   constexpr int SLAB = kThreads * EPT;
   const int R = 2 * a.K + 1;
   const int rowid = blockIdx.x, ch = blockIdx.y;
@@ -468,7 +469,7 @@ __global__ __launch_bounds__(kThreads) void stoch_stats_kernel(StochArgs a) {
 __global__ __launch_bounds__(kThreads) void stoch_decide_kernel(StochArgs a) {
   __shared__ float sM[2 * kMaxK + 1];
   __shared__ double sS[2 * kMaxK + 1];
-  __shared__ double etab[64];
+  __shared__ double etab[256];
   const int b = blockIdx.x;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int K = a.K, R = 2 * K + 1, nch = a.nch;
@@ -575,7 +576,7 @@ __device__ __forceinline__ float residual_of(float pt, float pd, int dtype) {
 template <typename T>
 __global__ __launch_bounds__(kThreads) void stoch_residual_kernel(StochArgs a) {
   __shared__ double red[kWaves];
-  __shared__ double etab[64];
+  __shared__ double etab[256];
   const int b = blockIdx.x, ch = blockIdx.y;
   const int32_t* dec = a.dec + 4 * b;
   if (dec[3] || dec[1] != 1) return;  // uniform: only sequences that rejected a draft
@@ -614,7 +615,7 @@ template <typename T, typename TQ>
 __global__ __launch_bounds__(kThreads) void stoch_sample_kernel(StochArgs a) {
   __shared__ uint64_t red[kWaves];
   __shared__ double redd[kWaves];
-  __shared__ double etab[64];
+  __shared__ double etab[256];
   const int b = blockIdx.x, ch = blockIdx.y, j = blockIdx.z;
   const int32_t* dec = a.dec + 4 * b;
   if (dec[3]) return;  // greedy sequence: finished by the accept walk

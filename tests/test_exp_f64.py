@@ -1,7 +1,7 @@
 """The fp64 exp of the acceptance kernels (naivllm_amd/csrc/exp_f64.h),
 compiled for the CPU from the same header: every table entry is the double
-nearest 2^(j/64) (60-digit decimal arithmetic), the reduction constants
-split ln2/64 exactly, and over a million seeded arguments in [-745, 0] the
+nearest 2^(j/256) (60-digit decimal arithmetic), the reduction constants
+split ln2/256 exactly, and over a million seeded arguments in [-745, 0] the
 result is within 2 ulps of the 80-bit expl value; 0 and -0 give 1, and
 -inf, NaN and arguments past the underflow edge give exactly 0."""
 
@@ -35,7 +35,7 @@ int main() {
     double t = -745.0 * (double)(s >> 11) / 9007199254740992.0;
     if (i % 4 == 1) t = -30.0 * (double)(s >> 11) / 9007199254740992.0;  // where softmax mass lives
     if (i % 4 == 2) t = -0.02 * (double)(s >> 11) / 9007199254740992.0;  // near the table nodes
-    const double got = nsv_exp_nonpos(t, kExp2Frac64);
+    const double got = nsv_exp_nonpos(t, kExp2Frac256);
     const long double want = expl((long double)t);
     if (want < 2.2250738585072014e-308L) continue;  // subnormal results: absolute error only
     const double e = ulps(got, want);
@@ -43,7 +43,7 @@ int main() {
   }
   std::printf("%.6f %.17g\n", worst, at);
   const double sp[6] = {0.0, -0.0, -INFINITY, NAN, -745.2, -1e300};
-  for (double t : sp) std::printf("%a\n", nsv_exp_nonpos(t, kExp2Frac64));
+  for (double t : sp) std::printf("%a\n", nsv_exp_nonpos(t, kExp2Frac256));
   return 0;
 }
 """
@@ -51,7 +51,7 @@ int main() {
 
 def table_from_header():
     text = HDR.read_text()
-    body = text[text.index("kExp2Frac64[64] = {") + len("kExp2Frac64[64] = {"):]
+    body = text[text.index("kExp2Frac256[256] = {") + len("kExp2Frac256[256] = {"):]
     body = body[:body.index("};")]
     return [float.fromhex(x.strip()) for x in body.split(",") if x.strip()]
 
@@ -66,15 +66,15 @@ def test_table_and_split_constants_are_exact():
     getcontext().prec = 60
     ln2 = Decimal(2).ln()
     tab = table_from_header()
-    assert len(tab) == 64
+    assert len(tab) == 256
     for j, v in enumerate(tab):
-        assert v == float((Decimal(j) / 64 * ln2).exp()), j
-    L = ln2 / 64
+        assert v == float((Decimal(j) / 256 * ln2).exp()), j
+    L = ln2 / 256
     hi, lo = constant("kLhi"), constant("kLlo")
     assert hi == float(L)
     assert lo == float(L - Decimal(hi))
-    # L_hi's last bit is 2^-59, which keeps t - k*L_hi exact in one fma
-    assert (Decimal(hi) * 2 ** 59) % 1 == 0
+    # L_hi's last bit is 2^-61, which keeps t - k*L_hi exact in one fma
+    assert (Decimal(hi) * 2 ** 61) % 1 == 0
 
 
 @pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++")
