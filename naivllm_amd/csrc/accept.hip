@@ -184,6 +184,25 @@ __device__ __forceinline__ double block_sum_d(double v, double* red) {
   __syncthreads();
   return r;
 }
+// two sums through one exchange (each summed as block_sum_d sums it)
+__device__ __forceinline__ void block_sum2_d(double& u, double& v, double* red) {
+  u = wave_sum_d(u);
+  v = wave_sum_d(v);
+  const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (lane == 0) {
+    red[w] = u;
+    red[kWaves + w] = v;
+  }
+  __syncthreads();
+  double ru = 0.0, rv = 0.0;
+  for (int i = 0; i < kWaves; ++i) {  // fixed order: deterministic
+    ru += red[i];
+    rv += red[kWaves + i];
+  }
+  __syncthreads();
+  u = ru;
+  v = rv;
+}
 __device__ __forceinline__ float block_max_f(float v, float* red) {
   v = wave_max_f(v);
   const int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -575,7 +594,7 @@ __device__ __forceinline__ float residual_of(float pt, float pd, int dtype) {
 // row of sequences that rejected a draft
 template <typename T>
 __global__ __launch_bounds__(kThreads) void stoch_residual_kernel(StochArgs a) {
-  __shared__ double red[kWaves];
+  __shared__ double red[2 * kWaves];
   __shared__ double etab[256];
   const int b = blockIdx.x, ch = blockIdx.y;
   const int32_t* dec = a.dec + 4 * b;
@@ -600,8 +619,7 @@ __global__ __launch_bounds__(kThreads) void stoch_residual_kernel(StochArgs a) {
     sr += (double)residual_of(pt, pd, a.cdtype);
     sp += (double)pt;
   }
-  sr = block_sum_d(sr, red);
-  sp = block_sum_d(sp, red);
+  block_sum2_d(sr, sp, red);
   if (threadIdx.x == 0) {
     a.res_part[((int64_t)b * a.nch2 + ch) * 2 + 0] = sr;
     a.res_part[((int64_t)b * a.nch2 + ch) * 2 + 1] = sp;
@@ -614,7 +632,7 @@ __global__ __launch_bounds__(kThreads) void stoch_residual_kernel(StochArgs a) {
 template <typename T, typename TQ>
 __global__ __launch_bounds__(kThreads) void stoch_sample_kernel(StochArgs a) {
   __shared__ uint64_t red[kWaves];
-  __shared__ double redd[kWaves];
+  __shared__ double redd[2 * kWaves];
   __shared__ double etab[256];
   const int b = blockIdx.x, ch = blockIdx.y, j = blockIdx.z;
   const int32_t* dec = a.dec + 4 * b;
@@ -647,8 +665,7 @@ __global__ __launch_bounds__(kThreads) void stoch_sample_kernel(StochArgs a) {
       tr += a.res_part[((int64_t)b * a.nch2 + k) * 2 + 0];
       tp += a.res_part[((int64_t)b * a.nch2 + k) * 2 + 1];
     }
-    tr = block_sum_d(tr, redd);  // its barriers also publish etab
-    tp = block_sum_d(tp, redd);
+    block_sum2_d(tr, tp, redd);  // its barriers also publish etab
     const float Sr = round_dt_d(tr, a.cdtype);
     const bool use_res = Sr > 0.f;
     const float S = use_res ? Sr : round_dt_d(tp, a.cdtype);
