@@ -300,7 +300,9 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
   // barrier later every output is the factor-weighted sum of the parked
   // slices.  Taken when the parking area fits beside the staging area.
   constexpr int PARK_FLOATS = NW * MP * RSTR;
-  constexpr bool PARK = SMEM + PARK_FLOATS * 4 + kMaxSplitPages * 4 + 2 * NW * MP * 4 + 3 * MP * 4 <= 159 * 1024;
+  constexpr int QBYTES = MP * DH * 2;  // the query rows, staged once for the 8 waves
+  constexpr bool PARK =
+      SMEM + QBYTES + PARK_FLOATS * 4 + kMaxSplitPages * 4 + 2 * NW * MP * 4 + 3 * MP * 4 <= 159 * 1024;
   // One LDS block, the small arrays first: their addresses then fit the
   // 16-bit offset field of the LDS instructions.
   struct __attribute__((aligned(16))) Lds {
@@ -311,6 +313,9 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
     int row_pos[MP];
     int ds_last;
     int pages[kMaxSplitPages];
+    // chunk X of query row m at slot X ^ (m % CPR): the 16 rows an operand
+    // read touches fall in distinct banks
+    __attribute__((aligned(16))) unsigned char q_lds[QBYTES];
     __attribute__((aligned(16))) unsigned char smem[SMEM];
     __attribute__((aligned(16))) float park[PARK ? PARK_FLOATS : 4];
   };
@@ -324,6 +329,7 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
   auto& pages = lds.pages;
   unsigned char* const smem = lds.smem;
   float* const park = lds.park;
+  unsigned char* const q_lds = lds.q_lds;
 
   // ---- workgroup -> (pair, dq, split): grid (8 P8, dqc, splits), so
   // workgroup (z dqc + y) 8 P8 + x runs on XCD x % 8 -- every workgroup of a
@@ -373,7 +379,14 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
     if (j < npg) pages[j] = pv[i];
   }
 
+  // The query rows are loaded once per workgroup (16-byte chunks spread over
+  // the threads), staged in LDS and read back by every wave as the B operand
+  // of S^T: each wave loading them all put 8x the bytes through the CU's
+  // intake ahead of the first tiles (b1 9.27 -> 8.89 us, 3k-key contexts
+  // 10.39 -> 9.74).
+  constexpr int QPASS = (MP * CPR + NT - 1) / NT;  // 16-byte query chunks per thread
   bf16x8 qB[MT][KS];
+  u32x4 qt[QPASS];
   int qpos[MT];
   int qmin = 0x7fffffff;
   auto load_q = [&]() {
@@ -382,12 +395,34 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
       const int m = mt * 16 + c;
       const int g = div_small(m, a.QL), t = m - g * a.QL;
       const bool ok = (m < a.Mv) && (t < qlen);
+      qpos[mt] = load_pos(a.positions, ok ? q0 + t : 0);
+    }
+#pragma unroll
+    for (int i = 0; i < QPASS; ++i) {
+      const int idx = tid + i * NT;
+      const int m = idx / CPR, ch = idx % CPR;
+      const int g = div_small(m, a.QL), t = m - g * a.QL;
+      const bool ok = (idx < MP * CPR) && (m < a.Mv) && (t < qlen);
       const int row = ok ? q0 + t : 0;
       const int gg = ok ? g : 0;
-      qpos[mt] = load_pos(a.positions, row);
-      const bf16_t* qrow = (const bf16_t*)a.q + ((int64_t)row * a.H + hk * a.Gs + a.g0 + gg) * DH;
+      qt[i] = load16((const bf16_t*)a.q + ((int64_t)row * a.H + hk * a.Gs + a.g0 + gg) * DH + ch * 8);
+    }
+  };
+  auto store_q = [&]() {
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) qB[mt][ks] = as_bf16x8(load16(qrow + ks * 32 + g4 * 8));
+    for (int i = 0; i < QPASS; ++i) {
+      const int idx = tid + i * NT;
+      const int m = idx / CPR, ch = idx % CPR;
+      if (idx < MP * CPR) *reinterpret_cast<u32x4*>(q_lds + m * (DH * 2) + ((ch ^ (m % CPR)) << 4)) = qt[i];
+    }
+  };
+  auto read_q = [&]() {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int m = mt * 16 + c;
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        qB[mt][ks] = as_bf16x8(*reinterpret_cast<const u32x4*>(q_lds + m * (DH * 2) + (((ks * 4 + g4) ^ (m % CPR)) << 4)));
     }
   };
   auto finish_positions = [&]() {
@@ -438,11 +473,16 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
   };
 
   // Issue every load of wave-tile `it`.  Masked keys read the row of a key
-  // that exists (finite data, zero weight).  A tile without any key (past
-  // the split's end, or on an unmapped page) issues no load: such dummy
-  // loads, a few per wave at these short splits, queued behind the real
-  // tiles in the CU's address unit (b1: ~1.5 us before the waves merged).
-  auto issue = [&](Tile& T, int it) {
+  // that exists (finite data, zero weight).  The first tile is always
+  // issued (past the split's end it reads the pool's first row), so the
+  // compiler's waits up to the query-staging barrier stay exact and the
+  // barrier leaves it in flight; a later tile without any key (past the
+  // split's end, or on an unmapped page) issues no load: such dummy loads,
+  // a few per wave at these short splits, queued behind the real tiles in
+  // the CU's address unit (b1: ~1.5 us before the waves merged).  (Loads at
+  // an offset outside an empty buffer resource, which return zeros without
+  // a memory access, still took that address-unit time: 9.2 -> 10.4 us.)
+  auto issue = [&](Tile& T, int it, auto skip_empty) {
     T.n0 = tok_begin + (it * NW + w) * kTile;
     if constexpr (UPAGE) {
       int nvalid = min(max(tok_end - T.n0, 0), kTile);
@@ -451,7 +491,9 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
       if (pg < 0) nvalid = 0;
       T.nvalid = nvalid;
       T.kmask = nvalid >= kTile ? 0xffffffffull : ((1ull << nvalid) - 1);
-      if (nvalid == 0) return;  // uniform
+      if constexpr (decltype(skip_empty)::value) {
+        if (nvalid == 0) return;  // uniform
+      }
       // byte addressing: scalar page base + 32-bit lane offsets
       const size_t page_off = (size_t)(pg < 0 ? 0 : pg) * (size_t)page_elems * 2;
       const char* kp = (const char*)kbase + page_off;
@@ -478,7 +520,9 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
       const int pg = (lane < kTile && n < tok_end) ? pages[(n >> a.bs_log2) - pg0] : -1;
       T.kmask = __ballot(pg >= 0);
       T.nvalid = 0;
-      if (T.kmask == 0) return;  // uniform
+      if constexpr (decltype(skip_empty)::value) {
+        if (T.kmask == 0) return;  // uniform
+      }
       const int first = T.kmask ? __builtin_ctzll(T.kmask) : 0;
       const int pg_first = __shfl(pg, first, NSV_WAVE);
       const int64_t dflt = T.kmask ? (int64_t)pg_first * page_elems + (int64_t)((T.n0 + first) & bs_mask) * tok_stride
@@ -626,17 +670,25 @@ __global__ __launch_bounds__(kBf16Waves * 64, 1) void verify_attn_bf16_kernel(Ve
   Tile T[NS];
   load_q();
   __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int s = 0; s < NS; ++s) issue(T[s], s);
+  issue(T[0], 0, std::false_type{});
   __builtin_amdgcn_sched_barrier(0);
   finish_positions();
+  store_q();
+  lds_barrier();  // query rows visible; the first tile stays in flight
+  read_q();
+  __builtin_amdgcn_sched_barrier(0);
+  // the later stages after the staging (an issue that may be skipped
+  // before it would leave its waits inexact)
+#pragma unroll
+  for (int s = 1; s < NS; ++s) issue(T[s], s, std::true_type{});
+  __builtin_amdgcn_sched_barrier(0);
   for (int it = 0; it < niter; it += NS) {
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
       __builtin_amdgcn_sched_barrier(0);
       compute(T[s]);
       if (it == 0 && s == 0) NSV_STAMP_AT(a, 2);  // first tile computed
-      issue(T[s], it + s + NS);
+      issue(T[s], it + s + NS, std::true_type{});
     }
   }
   NSV_STAMP_AT(a, 3);  // key loop done (wave 0)
