@@ -425,6 +425,25 @@ int nsv_linear_decode(const void* x, const void* norm_w, const float* ss_in,
                       int epilogue, void* stream);
 int nsv_linear_decode_ss_rows(int M, int N);
 
+/* The LM head (reference: src/myvllm/layers/embedding_head.py:71-83,
+ * ParallelLMHead.forward's F.linear(x, weight) over the vocabulary rows) on
+ * a weight repacked once at load time.  nsv_lm_head_pack writes the [N, K]
+ * bf16 weight (N a multiple of 16, K of 1024, 2048 or 4096) into `packed`
+ * (N * K bf16, a separate buffer) in the streaming kernel's load order: 16-byte
+ * chunk ((t * K/256 + g) * 8 + s) * 64 + l holds row 16 t + (l % 16),
+ * elements 256 g + 32 s + 8 (l / 16) .. + 7.  nsv_lm_head computes
+ * y[M, N] = x[M, K] W^T from that copy (bf16, fp32 accumulation, the same
+ * MFMA operands and order as nsv_linear's streaming dispatch, so the same
+ * bits): each wave load reads 1 KiB in a row instead of half of 16 lines.
+ * nsv_lm_head_rows gives the most rows it takes for this shape on the
+ * current device (0: the shape is not one it streams); beyond that,
+ * NSV_ERR_UNSUPPORTED (the caller then uses nsv_linear or a library GEMM
+ * with the row-major weight).  The pack launches on `stream`; the head
+ * launches nothing but its kernel and allocates nothing. */
+int nsv_lm_head_rows(int N, int K);
+int nsv_lm_head_pack(const void* weight, void* packed, int N, int K, void* stream);
+int nsv_lm_head(const void* x, const void* packed, void* y, int M, int N, int K, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

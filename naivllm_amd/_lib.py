@@ -72,6 +72,9 @@ SIGNATURES: dict[str, tuple] = {
     "nsv_linear_decode": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_f32, _c_vp, _c_vp, _c_vp, _c_vp]
                           + [_c_int] * 4 + [_c_vp]),
     "nsv_linear_decode_ss_rows": (_c_int, [_c_int] * 2),
+    "nsv_lm_head_rows": (_c_int, [_c_int] * 2),
+    "nsv_lm_head_pack": (_c_int, [_c_vp, _c_vp, _c_int, _c_int, _c_vp]),
+    "nsv_lm_head": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_int, _c_int, _c_vp]),
     "nsv_commit": (
         _c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64] + [_c_vp] * 5 + [_c_int, _c_vp, _c_vp, _c_int, _c_int, _c_vp]),
 }

@@ -632,7 +632,9 @@ struct StreamArgs {
   int tiles;          // N / 16
 };
 
-template <int MT, int NG>  // NG = K / 256 load groups per tile
+// PACKED: the weights in the layout nsv_lm_head_pack writes, where each
+// load instruction of a wave reads 1 KiB in a row (below).
+template <int MT, int NG, bool PACKED>  // NG = K / 256 load groups per tile
 __global__ __launch_bounds__(kStreamWaves * 64, 1) void stream_linear_kernel(StreamArgs a) {
   extern __shared__ __attribute__((aligned(16))) unsigned char xs_raw[];  // [M][K + 8] bf16
   __asm__ volatile("" ::"s"(a.x), "s"(a.w), "s"(a.y), "s"(a.M), "s"(a.N), "s"(a.K), "s"(a.tiles));
@@ -677,11 +679,23 @@ __global__ __launch_bounds__(kStreamWaves * 64, 1) void stream_linear_kernel(Str
   const __amdgpu_buffer_rsrc_t wrs =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.w), (short)0, (int)((int64_t)a.N * K * 2), 0x00020000);
   const int w_end = (int)((int64_t)a.N * K * 2);
-  auto wrow = [&](int i) { return i < my_tiles ? ((((gw + i * nwaves) * 16 + c) * K) + 8 * g4) * 2 : w_end; };
+  // Row-major [N, K]: load s of a group gives each of the tile's 16 rows 64
+  // bytes, half of a 128-byte line, and the next load the other half.
+  // Packed: the tile's 16 rows stored in exactly this load order, so load s
+  // is 1 KiB in a row (whole lines).  MI355X, graph-replayed, the 0.6B head
+  // (311 MB): 58-60 -> 51 us at 9 rows, 77 -> 65 at 72; the 8B head: 232 ->
+  // 194 us at 9 rows.
+  constexpr int LSTEP = PACKED ? 1024 : 64;                     // bytes between a group's loads
+  constexpr int GSTEP = PACKED ? 8 * 1024 : kStreamKG * 2;      // bytes between a tile's groups
+  auto wrow = [&](int i) {
+    if (i >= my_tiles) return w_end;
+    const int t = gw + i * nwaves;
+    return PACKED ? t * 16 * K * 2 + lane * 16 : (((t * 16 + c) * K) + 8 * g4) * 2;
+  };
   auto issue = [&](u32x4 (&buf)[8], int off) {
 #pragma unroll
     for (int s = 0; s < 8; ++s)
-      buf[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, off + 64 * s, 0, kCpolNt));
+      buf[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wrs, off + LSTEP * s, 0, kCpolNt));
   };
   f32x4 acc[MT];
 #pragma unroll
@@ -715,11 +729,11 @@ __global__ __launch_bounds__(kStreamWaves * 64, 1) void stream_linear_kernel(Str
 #pragma unroll
     for (int kg = 0; kg < NG; kg += 2) {
       __builtin_amdgcn_sched_barrier(0);
-      issue(B, p + (kg + 1) * kStreamKG * 2);
+      issue(B, p + (kg + 1) * GSTEP);
       __builtin_amdgcn_sched_barrier(0);
       compute(A, kg);
       __builtin_amdgcn_sched_barrier(0);
-      issue(A, kg + 2 < NG ? p + (kg + 2) * kStreamKG * 2 : pn);
+      issue(A, kg + 2 < NG ? p + (kg + 2) * GSTEP : pn);
       __builtin_amdgcn_sched_barrier(0);
       compute(B, kg + 1);
     }
@@ -748,29 +762,57 @@ bool stream_wide(int M, int N, int K, bool norm, int epi, int cus) {
          (int64_t)N * K * 2 <= ((int64_t)1 << 31) - (1 << 20);  // weight byte offsets (and one group past the end) fit an int
 }
 
-template <int MT, int NG>
+template <int MT, int NG, bool PACKED>
 int launch_stream(const StreamArgs& a, int cus, hipStream_t s) {
   static int attr[64] = {0};  // per device: the dynamic LDS limit raised once
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return NSV_ERR_UNSUPPORTED;
   if (!attr[dev]) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&stream_linear_kernel<MT, NG>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&stream_linear_kernel<MT, NG, PACKED>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, kStreamLds) != hipSuccess)
       return nsv_launch_status();
     attr[dev] = 1;
   }
   const size_t lds = (size_t)a.M * (a.K + 8) * 2;
-  hipLaunchKernelGGL((stream_linear_kernel<MT, NG>), dim3(cus), dim3(kStreamWaves * 64), lds, s, a);
+  hipLaunchKernelGGL((stream_linear_kernel<MT, NG, PACKED>), dim3(cus), dim3(kStreamWaves * 64), lds, s, a);
   return nsv_launch_status();
 }
 
-template <int MT>
+template <int MT, bool PACKED>
 int launch_stream_k(const StreamArgs& a, int cus, hipStream_t s) {
   switch (a.K) {
-    case 1024: return launch_stream<MT, 4>(a, cus, s);
-    case 2048: return launch_stream<MT, 8>(a, cus, s);
-    default: return launch_stream<MT, 16>(a, cus, s);  // 4096 (stream_wide admits no other)
+    case 1024: return launch_stream<MT, 4, PACKED>(a, cus, s);
+    case 2048: return launch_stream<MT, 8, PACKED>(a, cus, s);
+    default: return launch_stream<MT, 16, PACKED>(a, cus, s);  // 4096 (stream_wide admits no other)
   }
+}
+
+template <bool PACKED>
+int launch_stream_rows(const StreamArgs& sa, int cus, hipStream_t st) {
+  switch ((sa.M + 15) / 16) {
+    case 1: return launch_stream_k<1, PACKED>(sa, cus, st);
+    case 2: return launch_stream_k<2, PACKED>(sa, cus, st);
+    case 3: return launch_stream_k<3, PACKED>(sa, cus, st);
+    case 4: return launch_stream_k<4, PACKED>(sa, cus, st);
+    default: return launch_stream_k<5, PACKED>(sa, cus, st);
+  }
+}
+
+// The packed LM-head layout: 16-byte chunk q = ((t NG + kg) 8 + s) 64 + l of
+// the output holds W[16 t + (l & 15)][256 kg + 32 s + 8 (l >> 4) .. + 7]:
+// tile t's 16 rows, load group kg, load s, lane l, in the streaming kernel's
+// MFMA operand order.  One thread per chunk.
+__global__ __launch_bounds__(256) void lm_head_pack_kernel(const u32x4* __restrict__ w, u32x4* __restrict__ out,
+                                                           int64_t chunks, int K) {
+  const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (q >= chunks) return;
+  const int l = (int)(q & 63), ld = (int)((q >> 6) & 7);
+  const int64_t rest = q >> 9;
+  const int ng = K / kStreamKG;
+  const int64_t t = rest / ng;
+  const int kg = (int)(rest - t * ng);
+  const int64_t src = ((t * 16 + (l & 15)) * K + kg * kStreamKG + 32 * ld + 8 * (l >> 4)) / 8;
+  out[q] = w[src];
 }
 
 
@@ -1008,15 +1050,7 @@ int nsv_linear(const void* x, const void* norm_w, const float* ss_in, int nss_in
   const bool norm = norm_w != nullptr;
   if (stream_wide(M, N, K, norm, epilogue, lin_device_cus())) {
     const StreamArgs sa{(const uint16_t*)x, (const uint16_t*)weight, (uint16_t*)y, M, N, K, N / kBN};
-    const int cus = lin_device_cus();
-    hipStream_t st = (hipStream_t)stream;
-    switch ((M + 15) / 16) {
-      case 1: return launch_stream_k<1>(sa, cus, st);
-      case 2: return launch_stream_k<2>(sa, cus, st);
-      case 3: return launch_stream_k<3>(sa, cus, st);
-      case 4: return launch_stream_k<4>(sa, cus, st);
-      default: return launch_stream_k<5>(sa, cus, st);
-    }
+    return launch_stream_rows<false>(sa, lin_device_cus(), (hipStream_t)stream);
   }
   const LinPlan p = linear_plan(M, N, K, norm, epilogue, lin_device_cus());
   const size_t need = linear_ws_bytes(p.ks, N);
@@ -1033,6 +1067,32 @@ int nsv_linear(const void* x, const void* norm_w, const float* ss_in, int nss_in
     case 4: return launch_linear<4>(a, p, norm, epilogue, s);
     default: return launch_linear<5>(a, p, norm, epilogue, s);
   }
+}
+
+int nsv_lm_head_rows(int N, int K) {
+  if (N <= 0 || N % kBN || (K != 1024 && K != 2048 && K != 4096)) return 0;
+  const int rows = min(kMaxRows, kStreamLds / ((K + 8) * 2));
+  if (!stream_wide(1, N, K, false, 0, lin_device_cus()) || (int64_t)rows * N * 2 >= ((int64_t)1 << 31)) return 0;
+  return rows;
+}
+
+int nsv_lm_head_pack(const void* weight, void* packed, int N, int K, void* stream) {
+  if (!weight || !packed || N <= 0 || K <= 0) return NSV_ERR_ARG;
+  if (N % kBN || (K != 1024 && K != 2048 && K != 4096)) return NSV_ERR_UNSUPPORTED;
+  if (weight == packed) return NSV_ERR_ARG;
+  const int64_t chunks = (int64_t)N * K / 8;
+  hipLaunchKernelGGL(lm_head_pack_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                     (const u32x4*)weight, (u32x4*)packed, chunks, K);
+  return nsv_launch_status();
+}
+
+int nsv_lm_head(const void* x, const void* packed, void* y, int M, int N, int K, void* stream) {
+  if (M < 0 || N <= 0 || K <= 0) return NSV_ERR_ARG;
+  if (M == 0) return NSV_OK;
+  if (!x || !packed || !y) return NSV_ERR_ARG;
+  if (M > nsv_lm_head_rows(N, K)) return NSV_ERR_UNSUPPORTED;
+  const StreamArgs sa{(const uint16_t*)x, (const uint16_t*)packed, (uint16_t*)y, M, N, K, N / kBN};
+  return launch_stream_rows<true>(sa, lin_device_cus(), (hipStream_t)stream);
 }
 
 }  // extern "C"

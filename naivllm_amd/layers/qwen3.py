@@ -15,7 +15,8 @@ add epilogue).  Wider batches run the projections on hipBLASLt between
 this library's residual-RMSNorm, epilogue, attention and SiLU kernels.  The
 LM head runs on this library's streaming kernel up to lm_head_rows() rows
 (79 at hidden 1024, 19 at hidden 4096: the activations staged in one CU's
-LDS), on hipBLASLt beyond.  Weights are random (seeded): no checkpoint is
+LDS), from a copy of its weight packed in that kernel's load order, and on
+hipBLASLt beyond.  Weights are random (seeded): no checkpoint is
 loaded.
 
 The forward takes the verify metadata explicitly (positions, slots, block
@@ -124,6 +125,19 @@ def ss_rows(M: int, N: int, K: int, has_norm: bool = False) -> int:
     """Rows of partial sums of r^2 a residual-epilogue linear writes (one per
     16- or 8-column tile of the output)."""
     return int(_lib.lib().nsv_linear_ss_rows(M, N, K, int(has_norm)))
+
+
+def lm_head(x: torch.Tensor, packed: torch.Tensor, y: torch.Tensor) -> None:
+    """y = x @ W.T (ParallelLMHead.forward's F.linear) from W's copy written
+    by nsv_lm_head_pack, on the streaming kernel (nsv_lm_head): the same bits
+    as linear(x, W, y)."""
+    M, K = x.shape
+    N = y.shape[1]
+    if (tuple(packed.shape) != (N, K) or y.shape[0] != M or not (x.is_contiguous() and y.is_contiguous())
+            or not (x.dtype == packed.dtype == y.dtype == torch.bfloat16)):
+        raise ValueError("lm_head: x [M, K], packed [N, K] and y [M, N], contiguous bf16")
+    rc = _lib.lib().nsv_lm_head(x.data_ptr(), packed.data_ptr(), y.data_ptr(), M, N, K, _lib.stream_ptr(x.device))
+    _lib.check(rc, "lm_head")
 
 
 def linear(x: torch.Tensor, weight: torch.Tensor, y: torch.Tensor | None = None, *,
@@ -259,6 +273,18 @@ class Qwen3Verify:
             ))
         self.norm = torch.ones(E, device=self.device, dtype=dtype)
         self.lm_head = self.embed if cfg.tie_word_embeddings else w(cfg.vocab_size, E, scale=1.0 / math.sqrt(E))
+        # the LM head's weight also repacked once in the streaming kernel's
+        # load order (nsv_lm_head_pack) where this shape streams; the row-major
+        # weight stays for the embedding lookup and for more rows than that
+        self.lm_head_packed = None
+        self.lm_head_packed_rows = 0
+        if self.device.type == "cuda" and dtype == torch.bfloat16:
+            V = self.lm_head.shape[0]
+            self.lm_head_packed_rows = _lib.lib().nsv_lm_head_rows(V, E)
+            if self.lm_head_packed_rows > 0:
+                self.lm_head_packed = torch.empty_like(self.lm_head)
+                _lib.check(_lib.lib().nsv_lm_head_pack(self.lm_head.data_ptr(), self.lm_head_packed.data_ptr(), V, E,
+                                                       _lib.stream_ptr(self.device)), "lm_head_pack")
         self.rope = rope_cache(cfg, self.device)
         self.scale = 1.0 / math.sqrt(D)
         self.k_caches: list[torch.Tensor] = []
@@ -367,7 +393,10 @@ class Qwen3Verify:
         if T <= lm_head_rows(E):
             if logits_out is None:
                 logits_out = torch.empty(T, self.lm_head.shape[0], dtype=self.dtype, device=self.device)
-            linear(h, self.lm_head, logits_out)
+            if self.lm_head_packed is not None and T <= self.lm_head_packed_rows:
+                lm_head(h, self.lm_head_packed, logits_out)
+            else:
+                linear(h, self.lm_head, logits_out)
             return logits_out
         if logits_out is None:
             return F.linear(h, self.lm_head)

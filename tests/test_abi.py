@@ -252,6 +252,22 @@ def test_linear_plan_rejects_bad_shapes():
     assert h.nsv_linear_plan(9, 1024, 1024, 0, 3, 256, p, p, p) == -1  # no epilogue 3
 
 
+def test_lm_head_rows_and_argument_checks():
+    # host-side checks only: nothing is launched (no GPU here: 256 CUs assumed)
+    h = _lib.lib()
+    assert h.nsv_lm_head_rows(151936, 1024) == 79   # 79 x (1024 + 8) bf16 within 160 KiB of LDS
+    assert h.nsv_lm_head_rows(151936, 2048) == 39
+    assert h.nsv_lm_head_rows(151936, 4096) == 19
+    assert h.nsv_lm_head_rows(151936, 512) == 0     # K not streamed
+    assert h.nsv_lm_head_rows(4096, 1024) == 0      # fewer than 32 tiles per CU
+    assert h.nsv_lm_head_rows(151930, 1024) == 0    # N not a multiple of 16
+    assert h.nsv_lm_head(None, None, None, 0, 151936, 1024, None) == 0  # no rows: nothing to do
+    assert h.nsv_lm_head(None, None, None, 9, 151936, 1024, None) == -1
+    assert h.nsv_lm_head(1, 1, 1, 80, 151936, 1024, None) == -2         # past the row limit
+    assert h.nsv_lm_head_pack(1, 1, 151936, 1000, None) == -2
+    assert h.nsv_lm_head_pack(1, 1, 151936, 1024, None) == -1            # in place
+
+
 def test_no_alloc_entry_rejects_shapes_beyond_its_scratch():
     # a 64-sequence fp32 batch over 128-page tables needs ~19 MB of split
     # partials, beyond the allocation-free entry point's 16 MiB: rejected

@@ -18,6 +18,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
+from naivllm_amd import _lib
 from naivllm_amd.layers import qwen3 as qm
 
 pytestmark = pytest.mark.gpu
@@ -239,6 +240,38 @@ def test_linear_wide(M, N, K):
     y = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
     qm.linear(x, w, y)
     torch.testing.assert_close(y.float(), x.float() @ w.float().t(), **BF16)
+
+
+# The LM head on its packed weight (nsv_lm_head_pack + nsv_lm_head): the
+# packed copy is the permutation its header states (checked against torch's
+# view/permute of the row-major weight), and the head's output has the same
+# bits as nsv_linear's streaming dispatch on the row-major weight (the same
+# MFMA operands in the same order), at every WIDE shape it takes; one row
+# count past its limit is refused before any launch.
+@pytest.mark.parametrize("M,N,K", [c for c in WIDE if c[0] <= (79 if c[2] == 1024 else 39 if c[2] == 2048 else 19)])
+def test_lm_head_packed(M, N, K):
+    print(f"case: lm head packed M={M} N={N} K={K}", flush=True)
+    h = _lib.lib()
+    rows = h.nsv_lm_head_rows(N, K)
+    assert M <= rows
+    g = gen(M * 11 + N + K)
+    x = randn(g, M, K)
+    w = randn(g, N, K, scale=K ** -0.5)
+    packed = torch.full_like(w, float("nan"))
+    assert h.nsv_lm_head_pack(w.data_ptr(), packed.data_ptr(), N, K, _lib.stream_ptr(w.device)) == 0
+    want = w.view(N // 16, 16, K // 256, 8, 4, 8).permute(0, 2, 3, 4, 1, 5).reshape(N, K)
+    assert torch.equal(packed, want)
+    y = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+    qm.lm_head(x, packed, y)
+    y_ref = torch.full((M, N), float("nan"), dtype=torch.bfloat16, device="cuda")
+    qm.linear(x, w, y_ref)
+    torch.cuda.synchronize()
+    assert torch.equal(y, y_ref)
+    torch.testing.assert_close(y.float(), x.float() @ w.float().t(), **BF16)
+    big = torch.empty(rows + 1, K, dtype=torch.bfloat16, device="cuda")
+    out = torch.empty(rows + 1, N, dtype=torch.bfloat16, device="cuda")
+    assert h.nsv_lm_head(big.data_ptr(), packed.data_ptr(), out.data_ptr(), rows + 1, N, K,
+                         _lib.stream_ptr(w.device)) == -2
 
 
 # The decode-shaped kernel (nsv_linear_decode): one or two rows, each
