@@ -1866,7 +1866,9 @@ int make_plan(int B, int H, int Hkv, int D, int block_size, int max_blocks, int 
   // 2x faster.  So key-split from a sixteenth as many pairs as resident
   // workgroups, or when a table holds >= 4096 keys, or for one 16-row tile
   // of query rows (decode-shaped calls: at 8 pairs x 1.25k keys and 2 or 4
-  // rows per pair, 8.0 us against 9.4 for the d-sliced kernel and its merge).
+  // rows per pair, 8.0 us against 9.4 for the d-sliced kernel and its merge
+  // launch; with its in-kernel merge and query staging the d-sliced kernel
+  // there still made a self-drafting b1 round 7.30 -> 7.38 ms).
   const int64_t ks_slots = (int64_t)cus * (8 / kKsWaves);  // resident workgroups
   // (contexts under 2^22 keys: the kernel's split arithmetic, div_small)
   const bool ks_fits = p->MT <= 3 && block_size >= 16 && max_blocks <= kMaxSplitPages && max_ctx < (1 << 22) &&
