@@ -273,18 +273,7 @@ class Qwen3Verify:
             ))
         self.norm = torch.ones(E, device=self.device, dtype=dtype)
         self.lm_head = self.embed if cfg.tie_word_embeddings else w(cfg.vocab_size, E, scale=1.0 / math.sqrt(E))
-        # the LM head's weight also repacked once in the streaming kernel's
-        # load order (nsv_lm_head_pack) where this shape streams; the row-major
-        # weight stays for the embedding lookup and for more rows than that
-        self.lm_head_packed = None
-        self.lm_head_packed_rows = 0
-        if self.device.type == "cuda" and dtype == torch.bfloat16:
-            V = self.lm_head.shape[0]
-            self.lm_head_packed_rows = _lib.lib().nsv_lm_head_rows(V, E)
-            if self.lm_head_packed_rows > 0:
-                self.lm_head_packed = torch.empty_like(self.lm_head)
-                _lib.check(_lib.lib().nsv_lm_head_pack(self.lm_head.data_ptr(), self.lm_head_packed.data_ptr(), V, E,
-                                                       _lib.stream_ptr(self.device)), "lm_head_pack")
+        self.pack_lm_head()
         self.rope = rope_cache(cfg, self.device)
         self.scale = 1.0 / math.sqrt(D)
         self.k_caches: list[torch.Tensor] = []
@@ -295,6 +284,23 @@ class Qwen3Verify:
         # count, so its rows come out the same at every batch shape)
         self.decode_linears = False
 
+
+    def pack_lm_head(self) -> None:
+        """Repack the LM head's weight in the streaming kernel's load order
+        (nsv_lm_head_pack) where this shape streams; the row-major weight
+        stays for the embedding lookup and for more rows than that.  Called
+        once by the constructor; whoever replaces or edits self.lm_head
+        afterwards calls it again."""
+        self.lm_head_packed = None
+        self.lm_head_packed_rows = 0
+        if self.device.type != "cuda" or self.lm_head.dtype != torch.bfloat16:
+            return
+        V, E = self.lm_head.shape
+        self.lm_head_packed_rows = _lib.lib().nsv_lm_head_rows(V, E)
+        if self.lm_head_packed_rows > 0:
+            self.lm_head_packed = torch.empty_like(self.lm_head)
+            _lib.check(_lib.lib().nsv_lm_head_pack(self.lm_head.data_ptr(), self.lm_head_packed.data_ptr(), V, E,
+                                                   _lib.stream_ptr(self.device)), "lm_head_pack")
     def prefill_q_block(self) -> int:
         """Query rows per causal block of a prefill: the verify kernel serves
         up to 64 (GQA group x rows) per (sequence, kv head)."""
